@@ -1,0 +1,70 @@
+// Shared device/host helpers for the gfx950 kernels: bf16 conversion, wave64
+// reductions, error plumbing for the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#define BLT_WAVE 64
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+namespace blt {
+
+// ---- error plumbing (host) -------------------------------------------------
+void set_error(const std::string& msg);
+int fail(int status, const std::string& msg);
+int hip_fail(hipError_t e, const char* what);
+
+#define BLT_HIP_CHECK(expr)                                   \
+  do {                                                        \
+    hipError_t _e = (expr);                                   \
+    if (_e != hipSuccess) return ::blt::hip_fail(_e, #expr);  \
+  } while (0)
+
+// Check the launch that was just queued.
+#define BLT_LAUNCH_CHECK(what)                                \
+  do {                                                        \
+    hipError_t _e = hipGetLastError();                        \
+    if (_e != hipSuccess) return ::blt::hip_fail(_e, what);   \
+  } while (0)
+
+// ---- bf16 <-> f32 ------------------------------------------------------------
+__host__ __device__ inline float bf16_to_f32(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+
+// Round to nearest even; NaN stays NaN.
+__host__ __device__ inline uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+// ---- wave64 reductions -----------------------------------------------------
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, BLT_WAVE));
+  return v;
+}
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, BLT_WAVE);
+  return v;
+}
+
+inline unsigned ceil_div(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
+
+}  // namespace blt

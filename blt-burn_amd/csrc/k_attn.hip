@@ -1,0 +1,246 @@
+// Causal (optionally sliding-window) attention for gfx950, head_dim 64, bf16
+// operands on MFMA, f32 online softmax.
+//
+// One block = 4 wave64s = 128 queries of one (batch, head); K/V advance in
+// 64-key tiles through two LDS stages shared by the four waves.
+//
+// Each wave computes S^T = K . Q^T (v_mfma_f32_32x32x16_bf16, keys as rows,
+// its 32 queries as columns), so a lane owns one query column and 32 of the
+// 64 scores of that query: the running max and sum need one cross-lane step
+// (lane ^ 32) instead of a 32-lane reduction.  The output is accumulated
+// transposed, O^T = V^T . P^T, which keeps the per-query rescale factor in
+// the lane that owns the query.  The P^T registers feed the MFMA B operand
+// directly (no LDS round trip); V is stored transposed in LDS with a
+// 136-byte row pitch so the 8-byte operand reads are bank-conflict free.
+//
+// Masking follows the reference's additive causal mask (model.rs:153-165:
+// key j visible to query i iff j <= i), extended with a window W > 0
+// (also j > i - W).  Tiles entirely outside a wave's visible band are
+// skipped; fully visible tiles skip the per-element mask.
+#include "rowops.hpp"
+
+namespace blt {
+
+namespace {
+
+constexpr int BQ = 128;     // queries per block
+constexpr int BKV = 64;     // keys per tile
+constexpr int D = 64;       // head dim
+constexpr int VT_LD = 68;   // V^T row pitch in bf16 (136 B)
+constexpr int K_TILE = BKV * D;
+constexpr int V_TILE = D * VT_LD;
+constexpr int STAGE = K_TILE + V_TILE;
+
+__device__ inline int kswz(int key, int chunk) { return key * D + ((chunk ^ (key & 7)) << 3); }
+
+__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int lrow = lane & 31, lhalf = lane >> 5;
+
+  // XCD-aware order: consecutive query blocks of one (b, h) share K/V, so
+  // keep them on one XCD (dispatch places block i on XCD i % 8).
+  const int nqb = (int)((p.T + BQ - 1) / BQ);
+  const int64_t nb = (int64_t)nqb * p.H * p.B;
+  const int64_t bid = blockIdx.x;
+  const int64_t nb8 = nb & ~(int64_t)7;
+  const int64_t id = bid < nb8 ? (bid & 7) * (nb8 >> 3) + (bid >> 3) : bid;
+  const int qb = nqb - 1 - (int)(id % nqb);  // longest causal rows first
+  const int64_t bh = id / nqb;
+  const int64_t h = bh % p.H, b = bh / p.H;
+
+  const int64_t T = p.T;
+  const int64_t q0 = (int64_t)qb * BQ;
+  const int64_t qw = q0 + wid * 32;  // this wave's first query
+  const int window = p.causal ? p.window : 0;
+
+  // block key range
+  int64_t lo = 0, hi = T - 1;
+  if (p.causal) {
+    hi = q0 + BQ - 1 < T - 1 ? q0 + BQ - 1 : T - 1;
+    if (window > 0) lo = q0 - window + 1 > 0 ? q0 - window + 1 : 0;
+  }
+  const int t_begin = (int)(lo / BKV), t_end = (int)(hi / BKV);
+  // wave key range
+  int64_t wlo = 0, whi = T - 1;
+  if (p.causal) {
+    whi = qw + 31 < T - 1 ? qw + 31 : T - 1;
+    if (window > 0) wlo = qw - window + 1 > 0 ? qw - window + 1 : 0;
+  }
+  const bool wave_active = qw < T;
+  const int wt_begin = (int)(wlo / BKV), wt_end = (int)(whi / BKV);
+
+  const uint16_t* kbase = p.k + b * p.sb_k + h * p.sh_k;
+  const uint16_t* vbase = p.v + b * p.sb_v + h * p.sh_v;
+
+  // Q fragments (B operand of S^T = K . Q^T): query qw + lrow, d = 16*ks + 8*lhalf .. +8
+  const int64_t qi = qw + lrow;
+  bf16x8_t qf[4];
+  {
+    const uint16_t* qrow = p.q + b * p.sb_q + h * p.sh_q + (qi < T ? qi : 0) * p.st_q;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      uint4 t = qi < T ? *reinterpret_cast<const uint4*>(qrow + ks * 16 + lhalf * 8)
+                       : make_uint4(0, 0, 0, 0);
+      qf[ks] = __builtin_bit_cast(bf16x8_t, t);
+    }
+  }
+
+  // K/V tile staging: thread -> (key, 16-byte chunk) for two chunks each of K and V
+  uint4 rk[2], rv[2];
+  auto gload = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int id2 = tid + 256 * i, key = id2 >> 3, c = id2 & 7;
+      const int64_t kk = (int64_t)t * BKV + key;
+      if (kk < T) {
+        rk[i] = *reinterpret_cast<const uint4*>(kbase + kk * p.st_k + c * 8);
+        rv[i] = *reinterpret_cast<const uint4*>(vbase + kk * p.st_v + c * 8);
+      } else {
+        rk[i] = make_uint4(0, 0, 0, 0);
+        rv[i] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  auto sstore = [&](int stage) {
+    uint16_t* sk = lds + stage * STAGE;
+    uint16_t* sv = sk + K_TILE;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int id2 = tid + 256 * i, key = id2 >> 3, c = id2 & 7;
+      *reinterpret_cast<uint4*>(sk + kswz(key, c)) = rk[i];
+      const uint16_t* e = reinterpret_cast<const uint16_t*>(&rv[i]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sv[(c * 8 + j) * VT_LD + key] = e[j];
+    }
+  };
+
+  f32x16_t o[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[j][r] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  const float sl2 = 0.125f * 1.44269504088896340736f;  // 1/sqrt(64) * log2(e)
+
+  gload(t_begin);
+  sstore(0);
+  __syncthreads();
+
+  for (int t = t_begin; t <= t_end; ++t) {
+    if (t < t_end) gload(t + 1);
+    const int stage = (t - t_begin) & 1;
+    if (wave_active && t >= wt_begin && t <= wt_end) {
+      const uint16_t* sk = lds + stage * STAGE;
+      const uint16_t* sv = sk + K_TILE;
+      const int64_t kb = (int64_t)t * BKV;
+      // ---- S^T = K . Q^T (two 32-key sub-tiles) ----
+      f32x16_t s[2];
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[sub][r] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const bf16x8_t a =
+              *reinterpret_cast<const bf16x8_t*>(sk + kswz(sub * 32 + lrow, ks * 2 + lhalf));
+          s[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], s[sub], 0, 0, 0);
+        }
+      }
+      // ---- scale, mask, online softmax ----
+      const bool need_mask = (p.causal && kb + BKV - 1 > qw) ||
+                             (window > 0 && kb <= qw + 31 - window) || (kb + BKV > T);
+      float mt = -INFINITY;
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float x = s[sub][r] * sl2;
+          if (need_mask) {
+            const int64_t key = kb + sub * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+            bool vis = key < T;
+            if (p.causal) {
+              vis = vis && key <= qi;
+              if (window > 0) vis = vis && key > qi - window;
+            }
+            x = vis ? x : -INFINITY;
+          }
+          s[sub][r] = x;
+          mt = fmaxf(mt, x);
+        }
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      const float m_new = fmaxf(m, mt);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2f(m - m_use);
+      m = m_new;
+      float ls = 0.f;
+      bf16x8_t pb[2][2];
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          uint32_t w[4];
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            const float p0 = exp2f(s[sub][8 * u + e] - m_use);
+            const float p1 = exp2f(s[sub][8 * u + e + 1] - m_use);
+            ls += p0 + p1;
+            w[e >> 1] = pack_bf16x2(p0, p1);
+          }
+          pb[sub][u] = __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
+        }
+      l = l * alpha + ls;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
+      // ---- O^T += V^T . P^T ----
+#pragma unroll
+      for (int dsub = 0; dsub < 2; ++dsub) {
+        const uint16_t* vrow = sv + (dsub * 32 + lrow) * VT_LD;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int k0 = sub * 32 + u * 16 + 4 * lhalf;
+            const uint2 lo4 = *reinterpret_cast<const uint2*>(vrow + k0);
+            const uint2 hi4 = *reinterpret_cast<const uint2*>(vrow + k0 + 8);
+            const bf16x8_t a =
+                __builtin_bit_cast(bf16x8_t, make_uint4(lo4.x, lo4.y, hi4.x, hi4.y));
+            o[dsub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[sub][u], o[dsub], 0, 0, 0);
+          }
+      }
+    }
+    if (t < t_end) sstore((t + 1 - t_begin) & 1);
+    __syncthreads();
+  }
+
+  if (!wave_active || qi >= T) return;
+  const float lt = l + __shfl_xor(l, 32, 64);
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  uint16_t* orow = p.o + b * p.sb_o + h * p.sh_o + qi * p.st_o;
+#pragma unroll
+  for (int dsub = 0; dsub < 2; ++dsub)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d0 = dsub * 32 + 8 * j + 4 * lhalf;
+      uint2 w;
+      w.x = pack_bf16x2(o[dsub][4 * j] * inv, o[dsub][4 * j + 1] * inv);
+      w.y = pack_bf16x2(o[dsub][4 * j + 2] * inv, o[dsub][4 * j + 3] * inv);
+      *reinterpret_cast<uint2*>(orow + d0) = w;
+    }
+}
+
+}  // namespace
+
+int launch_attention(const AttnArgs& a, hipStream_t s) {
+  if (a.B == 0 || a.H == 0 || a.T == 0) return 0;
+  const int64_t nb = ((a.T + BQ - 1) / BQ) * a.H * a.B;
+  if (nb > 0x7fffffff) return fail(-2, "attention: grid too large");
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)nb), dim3(256), 0, s, a);
+  BLT_LAUNCH_CHECK("attn_fwd_kernel");
+  return 0;
+}
+
+}  // namespace blt

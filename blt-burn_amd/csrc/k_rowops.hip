@@ -1,0 +1,625 @@
+// Memory-bound row kernels for gfx950: softmax-entropy, RMSNorm(+L2), L2 norm,
+// softmax, SiLU*gate, coherence, embedding gather, RoPE, patch boundaries.
+//
+// Layout rule for every row kernel: one wave64 owns one row; lane j holds the
+// 4-element chunks j, j+64, j+128, ... of the row in registers (16-byte f32 /
+// 8-byte bf16 vector loads, fully coalesced), so each row is read from HBM
+// exactly once and all reductions are wave shuffles.  Rows wider than the
+// register budget fall back to a streaming variant that re-reads the row.
+#include "rowops.hpp"
+
+#include <math.h>
+
+namespace blt {
+
+// ---------------------------------------------------------------------------
+// element access
+// ---------------------------------------------------------------------------
+__device__ inline float ld1(const float* p, int64_t i) { return p[i]; }
+__device__ inline float ld1(const uint16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
+
+__device__ inline void ld4(const float* p, int64_t i, float v[4]) {
+  float4 t = *reinterpret_cast<const float4*>(p + i);
+  v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+}
+__device__ inline void ld4(const uint16_t* p, int64_t i, float v[4]) {
+  uint2 t = *reinterpret_cast<const uint2*>(p + i);
+  v[0] = bf16_to_f32((uint16_t)(t.x & 0xffff));
+  v[1] = bf16_to_f32((uint16_t)(t.x >> 16));
+  v[2] = bf16_to_f32((uint16_t)(t.y & 0xffff));
+  v[3] = bf16_to_f32((uint16_t)(t.y >> 16));
+}
+__device__ inline void st1(float* p, int64_t i, float v) { p[i] = v; }
+__device__ inline void st1(uint16_t* p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+__device__ inline void st4(float* p, int64_t i, const float v[4]) {
+  *reinterpret_cast<float4*>(p + i) = make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ inline void st4(uint16_t* p, int64_t i, const float v[4]) {
+  uint2 t;
+  t.x = pack_bf16x2(v[0], v[1]);
+  t.y = pack_bf16x2(v[2], v[3]);
+  *reinterpret_cast<uint2*>(p + i) = t;
+}
+
+// Row held in registers: VEC-element chunks, chunk c of lane l is row[(l + 64c)*VEC ..].
+template <typename T, int VEC, int NC>
+struct RowRegs {
+  float v[NC][VEC];
+  __device__ inline void load(const T* row, int n, int lane, float pad) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int e = (lane + BLT_WAVE * c) * VEC;
+      if (e < n) {
+        if constexpr (VEC == 4) ld4(row, e, v[c]);
+        else v[c][0] = ld1(row, e);
+      } else {
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) v[c][q] = pad;
+      }
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// softmax entropy: H = -sum exp(lsm) * lsm, lsm = x - max - log(sum exp(x - max))
+// (the NdArray form of patcher::entropy, patcher.rs:38-63)
+// ---------------------------------------------------------------------------
+template <typename T, int VEC, int NC>
+__global__ __launch_bounds__(256) void entropy_kernel(const T* __restrict__ logits,
+                                                      float* __restrict__ out, int64_t rows,
+                                                      int n) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  RowRegs<T, VEC, NC> r;
+  r.load(logits + row * n, n, lane, -INFINITY);
+  float m = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) m = fmaxf(m, r.v[c][q]);
+  m = wave_max(m);
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) s += __expf(r.v[c][q] - m);  // padding: exp(-inf) = 0
+  s = wave_sum(s);
+  const float lse = __logf(s);
+  float h = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) {
+      const int e = (lane + BLT_WAVE * c) * VEC + q;
+      if (e < n) {
+        const float lsm = (r.v[c][q] - m) - lse;
+        h += __expf(lsm) * lsm;
+      }
+    }
+  h = wave_sum(h);
+  if (lane == 0) out[row] = -h;
+}
+
+// Any width: three streaming passes over the row.
+template <typename T>
+__global__ __launch_bounds__(256) void entropy_stream_kernel(const T* __restrict__ logits,
+                                                             float* __restrict__ out,
+                                                             int64_t rows, int n) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* x = logits + row * n;
+  float m = -INFINITY;
+  for (int e = lane; e < n; e += BLT_WAVE) m = fmaxf(m, ld1(x, e));
+  m = wave_max(m);
+  float s = 0.f;
+  for (int e = lane; e < n; e += BLT_WAVE) s += __expf(ld1(x, e) - m);
+  s = wave_sum(s);
+  const float lse = __logf(s);
+  float h = 0.f;
+  for (int e = lane; e < n; e += BLT_WAVE) {
+    const float lsm = (ld1(x, e) - m) - lse;
+    h += __expf(lsm) * lsm;
+  }
+  h = wave_sum(h);
+  if (lane == 0) out[row] = -h;
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm with optional L2 norm of the input row.
+//   after_sqrt:  y = x / (sqrt(mean x^2) + eps) * w     (model.rs:758-770)
+//   inside_sqrt: y = x / sqrt(mean x^2 + eps) * w       (rms_norm_kernel.rs:40-43)
+// ---------------------------------------------------------------------------
+__device__ inline float rms_denominator(float ss, int n, float eps, int mode) {
+  const float ms = ss / (float)n;
+  return mode == 0 ? (sqrtf(ms) + eps) : sqrtf(ms + eps);
+}
+
+template <typename TX, typename TW, typename TY, int VEC, int NC>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const TX* __restrict__ x,
+                                                      const TW* __restrict__ w,
+                                                      TY* __restrict__ y,
+                                                      float* __restrict__ l2, int64_t rows,
+                                                      int n, float eps, int mode) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  RowRegs<TX, VEC, NC> r;
+  r.load(x + row * n, n, lane, 0.f);
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) ss += r.v[c][q] * r.v[c][q];
+  ss = wave_sum(ss);
+  const float den = rms_denominator(ss, n, eps, mode);
+  if (l2 != nullptr && lane == 0) l2[row] = sqrtf(ss);
+  if (y == nullptr) return;
+  TY* yr = y + row * n;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int e = (lane + BLT_WAVE * c) * VEC;
+    if (e < n) {
+      float wv[VEC], o[VEC];
+      if constexpr (VEC == 4) ld4(w, e, wv);
+      else wv[0] = ld1(w, e);
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) o[q] = (r.v[c][q] / den) * wv[q];
+      if constexpr (VEC == 4) st4(yr, e, o);
+      else st1(yr, e, o[0]);
+    }
+  }
+}
+
+template <typename TX, typename TW, typename TY>
+__global__ __launch_bounds__(256) void rmsnorm_stream_kernel(const TX* __restrict__ x,
+                                                             const TW* __restrict__ w,
+                                                             TY* __restrict__ y,
+                                                             float* __restrict__ l2,
+                                                             int64_t rows, int n, float eps,
+                                                             int mode) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const TX* xr = x + row * n;
+  float ss = 0.f;
+  for (int e = lane; e < n; e += BLT_WAVE) {
+    const float v = ld1(xr, e);
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  const float den = rms_denominator(ss, n, eps, mode);
+  if (l2 != nullptr && lane == 0) l2[row] = sqrtf(ss);
+  if (y == nullptr) return;
+  for (int e = lane; e < n; e += BLT_WAVE) st1(y + row * n, e, (ld1(xr, e) / den) * ld1(w, e));
+}
+
+// ---------------------------------------------------------------------------
+// softmax over the last dim: exp(x - max) / sum (Burn activation::softmax)
+// ---------------------------------------------------------------------------
+template <int VEC, int NC>
+__global__ __launch_bounds__(256) void softmax_kernel(const float* __restrict__ x,
+                                                      float* __restrict__ y, int64_t rows,
+                                                      int n) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  RowRegs<float, VEC, NC> r;
+  r.load(x + row * n, n, lane, -INFINITY);
+  float m = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) m = fmaxf(m, r.v[c][q]);
+  m = wave_max(m);
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) {
+      r.v[c][q] = __expf(r.v[c][q] - m);
+      s += r.v[c][q];
+    }
+  s = wave_sum(s);
+  float* yr = y + row * n;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int e = (lane + BLT_WAVE * c) * VEC;
+    if (e < n) {
+      float o[VEC];
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) o[q] = r.v[c][q] / s;
+      if constexpr (VEC == 4) st4(yr, e, o);
+      else st1(yr, e, o[0]);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void softmax_stream_kernel(const float* __restrict__ x,
+                                                             float* __restrict__ y,
+                                                             int64_t rows, int n) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* xr = x + row * n;
+  float m = -INFINITY;
+  for (int e = lane; e < n; e += BLT_WAVE) m = fmaxf(m, xr[e]);
+  m = wave_max(m);
+  float s = 0.f;
+  for (int e = lane; e < n; e += BLT_WAVE) s += __expf(xr[e] - m);
+  s = wave_sum(s);
+  for (int e = lane; e < n; e += BLT_WAVE) y[row * n + e] = __expf(xr[e] - m) / s;
+}
+
+// ---------------------------------------------------------------------------
+// elementwise: SiLU * gate, coherence
+// ---------------------------------------------------------------------------
+__device__ inline float silu_gate1(float g, float u) { return (g / (1.f + __expf(-g))) * u; }
+
+__global__ __launch_bounds__(256) void silu_gate_f32_kernel(const float* __restrict__ g,
+                                                            const float* __restrict__ u,
+                                                            float* __restrict__ out,
+                                                            int64_t n, int vec) {
+  const int64_t n4 = vec ? n / 4 : 0;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    float4 a = reinterpret_cast<const float4*>(g)[i];
+    float4 b = reinterpret_cast<const float4*>(u)[i];
+    reinterpret_cast<float4*>(out)[i] = make_float4(silu_gate1(a.x, b.x), silu_gate1(a.y, b.y),
+                                                    silu_gate1(a.z, b.z), silu_gate1(a.w, b.w));
+  }
+  for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    out[i] = silu_gate1(g[i], u[i]);
+}
+
+// 8 bf16 per thread per step (16-byte loads and stores).
+__global__ __launch_bounds__(256) void silu_gate_bf16_kernel(const uint16_t* __restrict__ g,
+                                                             const uint16_t* __restrict__ u,
+                                                             uint16_t* __restrict__ out,
+                                                             int64_t n, int vec) {
+  const int64_t n8 = vec ? n / 8 : 0;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += stride) {
+    uint4 a = reinterpret_cast<const uint4*>(g)[i];
+    uint4 b = reinterpret_cast<const uint4*>(u)[i];
+    const uint32_t* pa = reinterpret_cast<const uint32_t*>(&a);
+    const uint32_t* pb = reinterpret_cast<const uint32_t*>(&b);
+    uint4 o;
+    uint32_t* po = reinterpret_cast<uint32_t*>(&o);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float g0 = bf16_to_f32((uint16_t)(pa[k] & 0xffff)), g1 = bf16_to_f32((uint16_t)(pa[k] >> 16));
+      const float u0 = bf16_to_f32((uint16_t)(pb[k] & 0xffff)), u1 = bf16_to_f32((uint16_t)(pb[k] >> 16));
+      po[k] = pack_bf16x2(silu_gate1(g0, u0), silu_gate1(g1, u1));
+    }
+    reinterpret_cast<uint4*>(out)[i] = o;
+  }
+  for (int64_t i = n8 * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    out[i] = f32_to_bf16(silu_gate1(bf16_to_f32(g[i]), bf16_to_f32(u[i])));
+}
+
+__global__ __launch_bounds__(256) void coherence_kernel(const float* __restrict__ nrm,
+                                                        const float* __restrict__ ent,
+                                                        float* __restrict__ out, int64_t n,
+                                                        float eps) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    out[i] = (nrm[i] * nrm[i]) / (ent[i] + eps);
+}
+
+// ---------------------------------------------------------------------------
+// token embedding gather: x[r, :] = f32(W[clamp(tok[r]), :])   (nn::Embedding)
+// one wave per token row, 8-byte bf16 loads, 16-byte f32 stores.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ tok,
+                                                    const uint16_t* __restrict__ table,
+                                                    float* __restrict__ x, int64_t rows,
+                                                    int dim, int vocab) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  int t = tok[row];
+  t = t < 0 ? 0 : (t >= vocab ? vocab - 1 : t);
+  const uint16_t* src = table + (int64_t)t * dim;
+  float* dst = x + row * dim;
+  for (int e = lane * 4; e < dim; e += BLT_WAVE * 4) {
+    float v[4];
+    ld4(src, e, v);
+    st4(dst, e, v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RoPE (half-split pairs (m, m + d/2), model.rs:107-147) from a strided bf16
+// tensor into a dense [B, H, T, d] bf16 tensor.  One thread per (row, m).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rope_kernel(const uint16_t* __restrict__ src,
+                                                   uint16_t* __restrict__ dst,
+                                                   const float* __restrict__ cs, int64_t B,
+                                                   int64_t H, int64_t T, int d, int64_t sb,
+                                                   int64_t sh, int64_t st) {
+  const int half = d / 2;
+  const int64_t total = B * H * T * half;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int m = (int)(i % half);
+    const int64_t r = i / half;  // (b*H + h)*T + t
+    const int64_t t = r % T;
+    const int64_t bh = r / T;
+    const int64_t h = bh % H, b = bh / H;
+    const uint16_t* s = src + b * sb + h * sh + t * st;
+    const float x1 = bf16_to_f32(s[m]), x2 = bf16_to_f32(s[m + half]);
+    const float c = cs[(t * half + m) * 2], sn = cs[(t * half + m) * 2 + 1];
+    uint16_t* o = dst + r * d;
+    o[m] = f32_to_bf16(x1 * c - x2 * sn);
+    o[m + half] = f32_to_bf16(x1 * sn + x2 * c);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Patch boundaries: one 1024-thread block per batch row.
+//   flag[t] = 1 for t < 2; else monotonic: (H[t] - H[t-1]) > thr, global: H[t] > thr
+//   (patcher.rs:80-118; T = 1 -> [1], T = 2 -> [1, 1] fall out of the t < 2 rule).
+// Block-wide exclusive scan over the flags compacts the start indices
+// (patch_start_indices_cpu, patcher.rs:124-142); a second sweep turns the
+// starts into lengths (patch_lengths_from_start_indices, patcher.rs:144-164).
+// ---------------------------------------------------------------------------
+#define PB_THREADS 1024
+#define PB_ITEMS 8
+
+__global__ __launch_bounds__(PB_THREADS) void patch_boundary_kernel(
+    const float* __restrict__ H, int64_t T, float thr, int mode, int32_t* __restrict__ mask,
+    int32_t* __restrict__ starts, int32_t* __restrict__ lengths, int32_t* __restrict__ count) {
+  __shared__ int wave_tot[PB_THREADS / BLT_WAVE];
+  __shared__ int carry_s;
+  const int64_t b = blockIdx.x;
+  const float* h = H + b * T;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  if (tid == 0) carry_s = 0;
+  __syncthreads();
+  for (int64_t base = 0; base < T; base += (int64_t)PB_THREADS * PB_ITEMS) {
+    const int64_t p0 = base + (int64_t)tid * PB_ITEMS;
+    int flags[PB_ITEMS];
+    int local = 0;
+    float prev = (p0 >= 1 && p0 - 1 < T) ? h[p0 - 1] : 0.f;
+#pragma unroll
+    for (int k = 0; k < PB_ITEMS; ++k) {
+      const int64_t t = p0 + k;
+      int f = 0;
+      if (t < T) {
+        const float cur = h[t];
+        if (t < 2) f = 1;
+        else if (mode == 0) f = (cur - prev) > thr;
+        else f = cur > thr;
+        prev = cur;
+        if (mask) mask[b * T + t] = f;
+      }
+      flags[k] = f;
+      local += f;
+    }
+    // inclusive wave scan of per-thread counts
+    int incl = local;
+#pragma unroll
+    for (int off = 1; off < BLT_WAVE; off <<= 1) {
+      const int v = __shfl_up(incl, off, BLT_WAVE);
+      if (lane >= off) incl += v;
+    }
+    if (lane == BLT_WAVE - 1) wave_tot[wid] = incl;
+    __syncthreads();
+    if (wid == 0) {
+      int wt = lane < PB_THREADS / BLT_WAVE ? wave_tot[lane] : 0;
+      int wincl = wt;
+#pragma unroll
+      for (int off = 1; off < PB_THREADS / BLT_WAVE; off <<= 1) {
+        const int v = __shfl_up(wincl, off, BLT_WAVE);
+        if (lane >= off) wincl += v;
+      }
+      if (lane < PB_THREADS / BLT_WAVE) wave_tot[lane] = wincl - wt;  // exclusive
+    }
+    __syncthreads();
+    const int carry = carry_s;
+    int pos = carry + wave_tot[wid] + (incl - local);
+    if (starts) {
+#pragma unroll
+      for (int k = 0; k < PB_ITEMS; ++k)
+        if (flags[k]) starts[b * T + pos++] = (int32_t)(p0 + k);
+    }
+    __syncthreads();
+    if (tid == PB_THREADS - 1) carry_s = carry + wave_tot[wid] + incl;
+    __syncthreads();
+  }
+  const int n = carry_s;
+  if (tid == 0 && count) count[b] = n;
+  if (lengths && starts) {
+    __threadfence_block();
+    __syncthreads();
+    for (int i = tid; i < n; i += PB_THREADS) {
+      const int32_t s = starts[b * T + i];
+      const int32_t e = (i + 1 < n) ? starts[b * T + i + 1] : (int32_t)T;
+      lengths[b * T + i] = e - s;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host launchers
+// ---------------------------------------------------------------------------
+namespace {
+// Register-resident variants cover rows up to 64 * 4 * 8 = 2048 elements
+// (vector path, n % 4 == 0) or 64 * 16 = 1024 (scalar path); wider rows stream.
+template <class L>
+int dispatch_row(int n, bool vec_ok, const typename L::Args& a) {
+  if (n % 4 == 0 && vec_ok) {
+    switch ((n / 4 + 63) / 64) {
+      case 1: return L::template run<4, 1>(a);
+      case 2: return L::template run<4, 2>(a);
+      case 3: return L::template run<4, 3>(a);
+      case 4: return L::template run<4, 4>(a);
+      case 5: case 6: return L::template run<4, 6>(a);
+      case 7: case 8: return L::template run<4, 8>(a);
+      default: break;
+    }
+  } else if (n % 4 != 0 || !vec_ok) {
+    switch ((n + 63) / 64) {
+      case 1: return L::template run<1, 1>(a);
+      case 2: return L::template run<1, 2>(a);
+      case 3: case 4: return L::template run<1, 4>(a);
+      case 5: case 6: case 7: case 8: return L::template run<1, 8>(a);
+      case 9: case 10: case 11: case 12: case 13: case 14: case 15: case 16:
+        return L::template run<1, 16>(a);
+      default: break;
+    }
+  }
+  return L::stream(a);
+}
+
+template <typename T>
+struct EntropyL {
+  struct Args { const T* x; float* out; int64_t rows; int n; hipStream_t s; };
+  template <int VEC, int NC>
+  static int run(const Args& a) {
+    hipLaunchKernelGGL((entropy_kernel<T, VEC, NC>), dim3(ceil_div(a.rows, 4)), dim3(256), 0,
+                       a.s, a.x, a.out, a.rows, a.n);
+    BLT_LAUNCH_CHECK("entropy_kernel");
+    return 0;
+  }
+  static int stream(const Args& a) {
+    hipLaunchKernelGGL((entropy_stream_kernel<T>), dim3(ceil_div(a.rows, 4)), dim3(256), 0, a.s,
+                       a.x, a.out, a.rows, a.n);
+    BLT_LAUNCH_CHECK("entropy_stream_kernel");
+    return 0;
+  }
+};
+
+template <typename TX, typename TW, typename TY>
+struct RmsL {
+  struct Args {
+    const TX* x; const TW* w; TY* y; float* l2; int64_t rows; int n; float eps; int mode;
+    hipStream_t s;
+  };
+  template <int VEC, int NC>
+  static int run(const Args& a) {
+    hipLaunchKernelGGL((rmsnorm_kernel<TX, TW, TY, VEC, NC>), dim3(ceil_div(a.rows, 4)),
+                       dim3(256), 0, a.s, a.x, a.w, a.y, a.l2, a.rows, a.n, a.eps, a.mode);
+    BLT_LAUNCH_CHECK("rmsnorm_kernel");
+    return 0;
+  }
+  static int stream(const Args& a) {
+    hipLaunchKernelGGL((rmsnorm_stream_kernel<TX, TW, TY>), dim3(ceil_div(a.rows, 4)), dim3(256),
+                       0, a.s, a.x, a.w, a.y, a.l2, a.rows, a.n, a.eps, a.mode);
+    BLT_LAUNCH_CHECK("rmsnorm_stream_kernel");
+    return 0;
+  }
+};
+
+struct SoftmaxL {
+  struct Args { const float* x; float* y; int64_t rows; int n; hipStream_t s; };
+  template <int VEC, int NC>
+  static int run(const Args& a) {
+    hipLaunchKernelGGL((softmax_kernel<VEC, NC>), dim3(ceil_div(a.rows, 4)), dim3(256), 0, a.s,
+                       a.x, a.y, a.rows, a.n);
+    BLT_LAUNCH_CHECK("softmax_kernel");
+    return 0;
+  }
+  static int stream(const Args& a) {
+    hipLaunchKernelGGL(softmax_stream_kernel, dim3(ceil_div(a.rows, 4)), dim3(256), 0, a.s, a.x,
+                       a.y, a.rows, a.n);
+    BLT_LAUNCH_CHECK("softmax_stream_kernel");
+    return 0;
+  }
+};
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+unsigned elementwise_grid(int64_t work) {
+  int64_t g = (work + 255) / 256;
+  if (g > 256 * 64) g = 256 * 64;  // grid-stride beyond ~64 blocks per CU
+  return (unsigned)(g < 1 ? 1 : g);
+}
+}  // namespace
+
+int launch_entropy_f32(const float* x, float* out, int64_t rows, int n, hipStream_t s) {
+  if (rows == 0) return 0;
+  return dispatch_row<EntropyL<float>>(n, aligned(x, 16), {x, out, rows, n, s});
+}
+int launch_entropy_bf16(const uint16_t* x, float* out, int64_t rows, int n, hipStream_t s) {
+  if (rows == 0) return 0;
+  return dispatch_row<EntropyL<uint16_t>>(n, aligned(x, 8), {x, out, rows, n, s});
+}
+
+template <typename TX, typename TW, typename TY>
+int launch_rmsnorm(const TX* x, const TW* w, TY* y, float* l2, int64_t rows, int n, float eps,
+                   int mode, hipStream_t s) {
+  if (rows == 0) return 0;
+  const bool vec = aligned(x, 4 * sizeof(TX)) && aligned(w, 4 * sizeof(TW)) &&
+                   aligned(y, 4 * sizeof(TY));
+  return dispatch_row<RmsL<TX, TW, TY>>(n, vec, {x, w, y, l2, rows, n, eps, mode, s});
+}
+template int launch_rmsnorm<float, float, float>(const float*, const float*, float*, float*,
+                                                 int64_t, int, float, int, hipStream_t);
+template int launch_rmsnorm<uint16_t, uint16_t, uint16_t>(const uint16_t*, const uint16_t*,
+                                                          uint16_t*, float*, int64_t, int, float,
+                                                          int, hipStream_t);
+template int launch_rmsnorm<float, float, uint16_t>(const float*, const float*, uint16_t*,
+                                                    float*, int64_t, int, float, int,
+                                                    hipStream_t);
+
+int launch_softmax_f32(const float* x, float* y, int64_t rows, int n, hipStream_t s) {
+  if (rows == 0) return 0;
+  return dispatch_row<SoftmaxL>(n, aligned(x, 16) && aligned(y, 16), {x, y, rows, n, s});
+}
+
+int launch_silu_gate_f32(const float* g, const float* u, float* o, int64_t n, hipStream_t s) {
+  if (n == 0) return 0;
+  const int vec = aligned(g, 16) && aligned(u, 16) && aligned(o, 16);
+  hipLaunchKernelGGL(silu_gate_f32_kernel, dim3(elementwise_grid(n / 4 + 1)), dim3(256), 0, s, g,
+                     u, o, n, vec);
+  BLT_LAUNCH_CHECK("silu_gate_f32_kernel");
+  return 0;
+}
+int launch_silu_gate_bf16(const uint16_t* g, const uint16_t* u, uint16_t* o, int64_t n,
+                          hipStream_t s) {
+  if (n == 0) return 0;
+  const int vec = aligned(g, 16) && aligned(u, 16) && aligned(o, 16);
+  hipLaunchKernelGGL(silu_gate_bf16_kernel, dim3(elementwise_grid(n / 8 + 1)), dim3(256), 0, s,
+                     g, u, o, n, vec);
+  BLT_LAUNCH_CHECK("silu_gate_bf16_kernel");
+  return 0;
+}
+int launch_coherence(const float* nrm, const float* ent, float* out, int64_t n, float eps,
+                     hipStream_t s) {
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(coherence_kernel, dim3(elementwise_grid(n)), dim3(256), 0, s, nrm, ent, out,
+                     n, eps);
+  BLT_LAUNCH_CHECK("coherence_kernel");
+  return 0;
+}
+int launch_embed(const int32_t* tok, const uint16_t* table, float* x, int64_t rows, int dim,
+                 int vocab, hipStream_t s) {
+  if (rows == 0) return 0;
+  hipLaunchKernelGGL(embed_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, s, tok, table, x, rows,
+                     dim, vocab);
+  BLT_LAUNCH_CHECK("embed_kernel");
+  return 0;
+}
+int launch_rope(const uint16_t* src, uint16_t* dst, const float* cs, int64_t B, int64_t H,
+                int64_t T, int d, int64_t sb, int64_t sh, int64_t st, hipStream_t s) {
+  const int64_t total = B * H * T * (d / 2);
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(rope_kernel, dim3(elementwise_grid(total)), dim3(256), 0, s, src, dst, cs, B,
+                     H, T, d, sb, sh, st);
+  BLT_LAUNCH_CHECK("rope_kernel");
+  return 0;
+}
+int launch_patch_boundaries(const float* H, int64_t B, int64_t T, float thr, int mode,
+                            int32_t* mask, int32_t* starts, int32_t* lengths, int32_t* count,
+                            hipStream_t s) {
+  if (B == 0) return 0;
+  hipLaunchKernelGGL(patch_boundary_kernel, dim3((unsigned)B), dim3(PB_THREADS), 0, s, H, T, thr,
+                     mode, mask, starts, lengths, count);
+  BLT_LAUNCH_CHECK("patch_boundary_kernel");
+  return 0;
+}
+
+}  // namespace blt

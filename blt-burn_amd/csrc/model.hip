@@ -1,0 +1,312 @@
+// LMTransformer::forward_with_embeddings (model.rs:269-322) on gfx950.
+//
+// Device layout (one model handle per GPU):
+//   packed weights, bf16, "Bt" = [out, in] so both MFMA operands read K-contiguous:
+//     wqkv [L, 3D, D]   rows 0..D-1 = wq^T, D..2D-1 = wk^T, 2D..3D-1 = wv^T
+//     wo   [L, D, D]    wo^T
+//     w13  [L, 2F, D]   64-row groups: rows 64g..64g+31 = w1^T rows 32g..32g+31,
+//                       rows 64g+32..64g+63 = w3^T rows 32g..32g+31 (gate/up pairs
+//                       land in one lane of the GEMM epilogue)
+//     w2   [L, D, F]    w2^T
+//     wout [V, D]       output^T
+//   norm weights as f32; the RoPE cos/sin table [max_seqlen, 32, 2] f32.
+//   workspace for max_tokens rows: residual x f32 [M, D], normed bf16 [M, D],
+//   qkv bf16 [M, 3D] (q, k already rotated), attention out bf16 [M, D],
+//   FFN hidden bf16 [M, F], logits f32 [M, V], entropies/norms f32 [M].
+//
+// Per layer: rmsnorm -> QKV GEMM (+RoPE) -> attention -> O GEMM (+= residual)
+//            -> rmsnorm -> W1|W3 GEMM (+SiLU*gate) -> W2 GEMM (+= residual).
+#include "model.hpp"
+
+#include <math.h>
+#include <string.h>
+
+#include <vector>
+
+namespace blt {
+
+void rope_table_host(float* out, int head_dim, int max_seqlen, double theta) {
+  // precompute_freqs_cis (model.rs:24-52): inv_freq = 1f32 / (f32)theta^(2i/d),
+  // angle = (f32)pos * inv_freq, in f32, stored (cos, sin) per (pos, i).
+  const int half = head_dim / 2;
+  std::vector<float> inv(half);
+  for (int i = 0; i < half; ++i) {
+    const float p = (float)pow(theta, (double)(2 * i) / (double)head_dim);
+    inv[i] = 1.0f / p;
+  }
+  for (int pos = 0; pos < max_seqlen; ++pos) {
+    const float fp = (float)pos;
+    for (int i = 0; i < half; ++i) {
+      const float ang = fp * inv[i];
+      out[((int64_t)pos * half + i) * 2] = cosf(ang);
+      out[((int64_t)pos * half + i) * 2 + 1] = sinf(ang);
+    }
+  }
+}
+
+namespace {
+template <typename T>
+int dalloc(T** p, int64_t n, int64_t* total) {
+  if (n <= 0) {
+    *p = nullptr;
+    return 0;
+  }
+  hipError_t e = hipMalloc((void**)p, (size_t)n * sizeof(T));
+  if (e != hipSuccess) return fail(-4, std::string("hipMalloc failed: ") + hipGetErrorString(e));
+  *total += n * (int64_t)sizeof(T);
+  return 0;
+}
+}  // namespace
+
+int Model::mark(int stage, hipStream_t s) {
+  if (!profiling) return 0;
+  if (ev_used == ev_pool.size()) {
+    hipEvent_t e;
+    BLT_HIP_CHECK(hipEventCreate(&e));
+    ev_pool.push_back(e);
+  }
+  BLT_HIP_CHECK(hipEventRecord(ev_pool[ev_used], s));
+  ev_marks.emplace_back(stage, ev_used);
+  ev_stream = s;
+  ++ev_used;
+  return 0;
+}
+
+// Sum the time between consecutive marks per stage (stage -1 = the start
+// mark of a forward), then forget the marks.
+int Model::read_profile(double* ms, int64_t* launches, int n) {
+  for (int i = 0; i < n; ++i) {
+    ms[i] = 0.0;
+    launches[i] = 0;
+  }
+  if (!ev_marks.empty()) BLT_HIP_CHECK(hipEventSynchronize(ev_pool[ev_marks.back().second]));
+  for (size_t i = 1; i < ev_marks.size(); ++i) {
+    const int st = ev_marks[i].first;
+    if (st < 0) continue;
+    float t = 0.f;
+    BLT_HIP_CHECK(hipEventElapsedTime(&t, ev_pool[ev_marks[i - 1].second],
+                                      ev_pool[ev_marks[i].second]));
+    if (st < n) {
+      ms[st] += t;
+      launches[st] += 1;
+    }
+  }
+  ev_marks.clear();
+  ev_used = 0;
+  return 0;
+}
+
+Model::~Model() {
+  for (hipEvent_t e : ev_pool) (void)hipEventDestroy(e);
+  void* ptrs[] = {emb, attn_norm, ffn_norm, final_norm, wqkv, wo, w13, w2, wout, rope_cs,
+                  x, a, qkv, attn, hbuf, logits, ent, norms};
+  int prev = -1;
+  (void)hipGetDevice(&prev);
+  (void)hipSetDevice(device);
+  for (void* p : ptrs)
+    if (p) (void)hipFree(p);
+  if (prev >= 0) (void)hipSetDevice(prev);
+}
+
+int Model::create(int dev, const blt_model_config& c, const blt_model_weights& w,
+                  int64_t max_tok, Model** out) {
+  if (c.dim <= 0 || c.n_heads <= 0 || c.dim % c.n_heads != 0 || c.dim / c.n_heads != 64)
+    return fail(-2, "model: head_dim = dim / n_heads must be 64");
+  if (c.dim % 64 != 0) return fail(-2, "model: dim must be a multiple of 64");
+  if (c.ffn_hidden <= 0 || c.ffn_hidden % 64 != 0)
+    return fail(-2, "model: ffn_hidden must be a positive multiple of 64");
+  if (c.vocab <= 0 || c.n_layers < 0 || c.max_seqlen <= 0 || max_tok <= 0)
+    return fail(-2, "model: bad vocab / n_layers / max_seqlen / max_tokens");
+  if (c.window < 0) return fail(-2, "model: window must be >= 0");
+  if (!w.tok_embeddings || !w.norm || !w.output)
+    return fail(-1, "model: null embedding / norm / output weight");
+  if (c.n_layers > 0) {
+    const void* per_layer[] = {w.attention_norm, w.ffn_norm, w.wq, w.wk, w.wv,
+                               w.wo,             w.w1,       w.w2, w.w3};
+    for (const void* q : per_layer)
+      if (q == nullptr) return fail(-1, "model: null per-layer weight pointer");
+  }
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || dev < 0 || dev >= ndev)
+    return fail(-5, "model: no such HIP device");
+  BLT_HIP_CHECK(hipSetDevice(dev));
+
+  Model* m = new Model();
+  m->device = dev;
+  m->cfg = c;
+  m->max_tokens = max_tok;
+  const int64_t D = c.dim, F = c.ffn_hidden, V = c.vocab, L = c.n_layers;
+  int64_t& tb = m->bytes;
+  int rc = 0;
+  rc |= dalloc(&m->emb, V * D, &tb);
+  rc |= dalloc(&m->attn_norm, L * D, &tb);
+  rc |= dalloc(&m->ffn_norm, L * D, &tb);
+  rc |= dalloc(&m->final_norm, D, &tb);
+  rc |= dalloc(&m->wqkv, L * 3 * D * D, &tb);
+  rc |= dalloc(&m->wo, L * D * D, &tb);
+  rc |= dalloc(&m->w13, L * 2 * F * D, &tb);
+  rc |= dalloc(&m->w2, L * D * F, &tb);
+  rc |= dalloc(&m->wout, V * D, &tb);
+  rc |= dalloc(&m->rope_cs, (int64_t)c.max_seqlen * 64, &tb);
+  rc |= dalloc(&m->x, max_tok * D, &tb);
+  rc |= dalloc(&m->a, max_tok * D, &tb);
+  rc |= dalloc(&m->qkv, max_tok * 3 * D, &tb);
+  rc |= dalloc(&m->attn, max_tok * D, &tb);
+  rc |= dalloc(&m->hbuf, max_tok * F, &tb);
+  rc |= dalloc(&m->logits, max_tok * V, &tb);
+  rc |= dalloc(&m->ent, max_tok, &tb);
+  rc |= dalloc(&m->norms, max_tok, &tb);
+  if (rc) {
+    delete m;
+    return -4;
+  }
+
+  // ---- pack on the host, copy once ----
+  auto up = [&](void* dst, const void* src, int64_t bytes) -> int {
+    BLT_HIP_CHECK(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyHostToDevice));
+    return 0;
+  };
+  auto to_f32 = [](const uint16_t* s, int64_t n) {
+    std::vector<float> v(n);
+    for (int64_t i = 0; i < n; ++i) v[i] = bf16_to_f32(s[i]);
+    return v;
+  };
+  // Bt[n][k] = W[k][n] for a [K, N] Burn Linear weight
+  auto transpose_into = [](uint16_t* dst, const uint16_t* W, int64_t K, int64_t N) {
+    for (int64_t k = 0; k < K; ++k)
+      for (int64_t n = 0; n < N; ++n) dst[n * K + k] = W[k * N + n];
+  };
+  if ((rc = up(m->emb, w.tok_embeddings, V * D * 2))) { delete m; return rc; }
+  {
+    std::vector<float> f = to_f32(w.norm, D);
+    if ((rc = up(m->final_norm, f.data(), D * 4))) { delete m; return rc; }
+    std::vector<uint16_t> t(V * D);
+    transpose_into(t.data(), w.output, D, V);
+    if ((rc = up(m->wout, t.data(), V * D * 2))) { delete m; return rc; }
+  }
+  if (L > 0) {
+    std::vector<float> f = to_f32(w.attention_norm, L * D);
+    if ((rc = up(m->attn_norm, f.data(), L * D * 4))) { delete m; return rc; }
+    f = to_f32(w.ffn_norm, L * D);
+    if ((rc = up(m->ffn_norm, f.data(), L * D * 4))) { delete m; return rc; }
+  }
+  std::vector<uint16_t> tmp;
+  for (int64_t l = 0; l < L; ++l) {
+    tmp.assign(3 * D * D, 0);
+    transpose_into(tmp.data(), w.wq + l * D * D, D, D);
+    transpose_into(tmp.data() + D * D, w.wk + l * D * D, D, D);
+    transpose_into(tmp.data() + 2 * D * D, w.wv + l * D * D, D, D);
+    if ((rc = up(m->wqkv + l * 3 * D * D, tmp.data(), 3 * D * D * 2))) { delete m; return rc; }
+    tmp.assign(D * D, 0);
+    transpose_into(tmp.data(), w.wo + l * D * D, D, D);
+    if ((rc = up(m->wo + l * D * D, tmp.data(), D * D * 2))) { delete m; return rc; }
+    // w13 interleave in 32-row groups
+    tmp.assign(2 * F * D, 0);
+    const uint16_t* w1 = w.w1 + l * D * F;
+    const uint16_t* w3 = w.w3 + l * D * F;
+    for (int64_t n = 0; n < 2 * F; ++n) {
+      const int64_t g = n / 64, cc = n % 64;
+      const uint16_t* src = cc < 32 ? w1 : w3;
+      const int64_t col = 32 * g + (cc & 31);
+      for (int64_t k = 0; k < D; ++k) tmp[n * D + k] = src[k * F + col];
+    }
+    if ((rc = up(m->w13 + l * 2 * F * D, tmp.data(), 2 * F * D * 2))) { delete m; return rc; }
+    tmp.assign(D * F, 0);
+    transpose_into(tmp.data(), w.w2 + l * F * D, F, D);
+    if ((rc = up(m->w2 + l * D * F, tmp.data(), D * F * 2))) { delete m; return rc; }
+  }
+  {
+    std::vector<float> cs((size_t)c.max_seqlen * 64);
+    rope_table_host(cs.data(), 64, c.max_seqlen, c.rope_theta);
+    if ((rc = up(m->rope_cs, cs.data(), (int64_t)cs.size() * 4))) { delete m; return rc; }
+  }
+  *out = m;
+  return 0;
+}
+
+int Model::forward(const int32_t* tokens, int64_t B, int64_t T, const blt_model_outputs& o,
+                   hipStream_t s) {
+  if (tokens == nullptr) return fail(-1, "forward: tokens is null");
+  if (B < 0 || T < 0) return fail(-2, "forward: negative shape");
+  if (T > cfg.max_seqlen) return fail(-2, "forward: seq_len exceeds max_seqlen");
+  const int64_t M = B * T;
+  if (M > max_tokens) return fail(-2, "forward: B*T exceeds the model's max_tokens");
+  if (M == 0) return 0;
+  BLT_HIP_CHECK(hipSetDevice(device));
+  const int64_t D = cfg.dim, F = cfg.ffn_hidden, V = cfg.vocab, H = cfg.n_heads;
+  // The residual stream lives in the caller's pre_norm_embeddings buffer when
+  // one is given (it is exactly the value to return), else in the workspace.
+  float* xr = o.pre_norm_embeddings ? o.pre_norm_embeddings : x;
+  int rc;
+  if (profiling && ev_used + 16 * (cfg.n_layers + 1) > 4096) {
+    // unread marks pile up: keep the pool bounded by dropping them
+    ev_marks.clear();
+    ev_used = 0;
+  }
+  if ((rc = mark(-1, s))) return rc;
+  if ((rc = launch_embed(tokens, emb, xr, M, (int)D, (int)V, s))) return rc;
+  if ((rc = mark(BLT_STAGE_EMBED, s))) return rc;
+  for (int64_t l = 0; l < cfg.n_layers; ++l) {
+    if ((rc = launch_rmsnorm<float, float, uint16_t>(xr, attn_norm + l * D, a, nullptr, M, (int)D,
+                                                     cfg.norm_eps, 0, s)))
+      return rc;
+    if ((rc = mark(BLT_STAGE_RMSNORM, s))) return rc;
+    GemmArgs g{};
+    g.A = a; g.Bt = wqkv + l * 3 * D * D; g.C = qkv;
+    g.M = M; g.N = 3 * D; g.K = D; g.lda = D; g.ldb = D; g.ldc = 3 * D;
+    g.epi = EPI_QKV_ROPE; g.rope_cols = (int)(2 * D); g.seq_len = T; g.rope_cs = rope_cs;
+    if ((rc = launch_gemm(g, s))) return rc;
+    if ((rc = mark(BLT_STAGE_QKV_GEMM, s))) return rc;
+    AttnArgs at{};
+    at.q = qkv; at.k = qkv + D; at.v = qkv + 2 * D; at.o = attn;
+    at.B = B; at.H = H; at.T = T;
+    at.sb_q = T * 3 * D; at.sh_q = 64; at.st_q = 3 * D;
+    at.sb_k = T * 3 * D; at.sh_k = 64; at.st_k = 3 * D;
+    at.sb_v = T * 3 * D; at.sh_v = 64; at.st_v = 3 * D;
+    at.sb_o = T * D; at.sh_o = 64; at.st_o = D;
+    at.causal = 1; at.window = cfg.window;
+    if ((rc = launch_attention(at, s))) return rc;
+    if ((rc = mark(BLT_STAGE_ATTENTION, s))) return rc;
+    g = GemmArgs{};
+    g.A = attn; g.Bt = wo + l * D * D; g.C = xr;
+    g.M = M; g.N = D; g.K = D; g.lda = D; g.ldb = D; g.ldc = D; g.epi = EPI_RESID_F32;
+    if ((rc = launch_gemm(g, s))) return rc;
+    if ((rc = mark(BLT_STAGE_O_GEMM, s))) return rc;
+    if ((rc = launch_rmsnorm<float, float, uint16_t>(xr, ffn_norm + l * D, a, nullptr, M, (int)D,
+                                                     cfg.norm_eps, 0, s)))
+      return rc;
+    if ((rc = mark(BLT_STAGE_RMSNORM, s))) return rc;
+    g = GemmArgs{};
+    g.A = a; g.Bt = w13 + l * 2 * F * D; g.C = hbuf;
+    g.M = M; g.N = 2 * F; g.K = D; g.lda = D; g.ldb = D; g.ldc = F; g.epi = EPI_SILU_GATE;
+    if ((rc = launch_gemm(g, s))) return rc;
+    if ((rc = mark(BLT_STAGE_W13_GEMM, s))) return rc;
+    g = GemmArgs{};
+    g.A = hbuf; g.Bt = w2 + l * D * F; g.C = xr;
+    g.M = M; g.N = D; g.K = F; g.lda = F; g.ldb = F; g.ldc = D; g.epi = EPI_RESID_F32;
+    if ((rc = launch_gemm(g, s))) return rc;
+    if ((rc = mark(BLT_STAGE_W2_GEMM, s))) return rc;
+  }
+  // pre-norm L2 norms fused with the final RMSNorm (one read of the residual)
+  float* nr = o.embedding_norms ? o.embedding_norms : norms;
+  if ((rc = launch_rmsnorm<float, float, uint16_t>(xr, final_norm, a, nr, M, (int)D, cfg.norm_eps,
+                                                   0, s)))
+    return rc;
+  if ((rc = mark(BLT_STAGE_FINAL_NORM, s))) return rc;
+  float* lg = o.logits ? o.logits : logits;
+  GemmArgs g{};
+  g.A = a; g.Bt = wout; g.C = lg;
+  g.M = M; g.N = V; g.K = D; g.lda = D; g.ldb = D; g.ldc = V; g.epi = EPI_F32; g.n_valid = (int)V;
+  if ((rc = launch_gemm(g, s))) return rc;
+  if ((rc = mark(BLT_STAGE_HEAD_GEMM, s))) return rc;
+  float* en = o.entropies ? o.entropies : ent;
+  if ((rc = launch_entropy_f32(lg, en, M, (int)V, s))) return rc;
+  if ((rc = mark(BLT_STAGE_ENTROPY, s))) return rc;
+  if (o.coherence_scores) {
+    if ((rc = launch_coherence(nr, en, o.coherence_scores, M, 1e-6f, s))) return rc;
+    if ((rc = mark(BLT_STAGE_COHERENCE, s))) return rc;
+  }
+  return 0;
+}
+
+}  // namespace blt

@@ -1,0 +1,61 @@
+// Host launchers of the kernels (each returns 0 or a negative blt_status).
+#pragma once
+#include "common.hpp"
+
+namespace blt {
+
+// k_rowops.hip
+int launch_entropy_f32(const float* x, float* out, int64_t rows, int n, hipStream_t s);
+int launch_entropy_bf16(const uint16_t* x, float* out, int64_t rows, int n, hipStream_t s);
+template <typename TX, typename TW, typename TY>
+int launch_rmsnorm(const TX* x, const TW* w, TY* y, float* l2, int64_t rows, int n, float eps,
+                   int mode, hipStream_t s);
+int launch_softmax_f32(const float* x, float* y, int64_t rows, int n, hipStream_t s);
+int launch_silu_gate_f32(const float* g, const float* u, float* o, int64_t n, hipStream_t s);
+int launch_silu_gate_bf16(const uint16_t* g, const uint16_t* u, uint16_t* o, int64_t n,
+                          hipStream_t s);
+int launch_coherence(const float* nrm, const float* ent, float* out, int64_t n, float eps,
+                     hipStream_t s);
+int launch_embed(const int32_t* tok, const uint16_t* table, float* x, int64_t rows, int dim,
+                 int vocab, hipStream_t s);
+int launch_rope(const uint16_t* src, uint16_t* dst, const float* cs, int64_t B, int64_t H,
+                int64_t T, int d, int64_t sb, int64_t sh, int64_t st, hipStream_t s);
+int launch_patch_boundaries(const float* H, int64_t B, int64_t T, float thr, int mode,
+                            int32_t* mask, int32_t* starts, int32_t* lengths, int32_t* count,
+                            hipStream_t s);
+
+// k_gemm.hip -----------------------------------------------------------------
+// C[M, N] = A[M, K] . Bt[N, K]^T with bf16 operands and f32 accumulation; the
+// epilogue decides what is written.  K % 64 == 0, N % 64 == 0 (Bt padded with
+// zero rows by the caller where the logical N is smaller).
+enum GemmEpi {
+  EPI_BF16 = 0,      // C bf16 [M, ldc]
+  EPI_F32 = 1,       // C f32 [M, ldc], columns >= n_valid dropped
+  EPI_RESID_F32 = 2, // R f32 [M, ldc] += acc (in place)
+  EPI_QKV_ROPE = 3,  // bf16 out; columns < rope_cols rotated (half-split pairs within 64-wide heads)
+  EPI_SILU_GATE = 4  // Bt interleaved in 32-column (gate, up) groups; out bf16 [M, N/2]
+};
+struct GemmArgs {
+  const uint16_t* A;
+  const uint16_t* Bt;
+  void* C;
+  int64_t M, N, K;
+  int64_t lda, ldb, ldc;
+  int epi;
+  int n_valid;      // EPI_F32
+  int rope_cols;    // EPI_QKV_ROPE
+  int64_t seq_len;  // EPI_QKV_ROPE: position = row % seq_len
+  const float* rope_cs;  // [max_seqlen, 32, 2]
+};
+int launch_gemm(const GemmArgs& a, hipStream_t s);
+
+// k_attn.hip -----------------------------------------------------------------
+struct AttnArgs {
+  const uint16_t* q; const uint16_t* k; const uint16_t* v; uint16_t* o;
+  int64_t B, H, T;
+  int64_t sb_q, sh_q, st_q, sb_k, sh_k, st_k, sb_v, sh_v, st_v, sb_o, sh_o, st_o;
+  int causal, window;
+};
+int launch_attention(const AttnArgs& a, hipStream_t s);
+
+}  // namespace blt

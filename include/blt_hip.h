@@ -1,0 +1,251 @@
+/*
+ * blt_hip.h — C ABI of the MI355X (gfx950) entropy-patching library.
+ *
+ * Drop-in boundary for blt-burn's entropy-patching hot path.  Every entry
+ * point below names the reference interface it replaces (file:line in
+ * SashimiSaketoro/blt-burn).  Conventions:
+ *
+ *   - All tensors are caller-owned, dense, row-major device buffers.  The
+ *     library never frees caller memory; a model handle owns only its packed
+ *     weights and its workspace.
+ *   - bf16 tensors are passed as uint16_t* holding IEEE bfloat16 bits.
+ *   - Every call is stream-ordered: `stream` is a hipStream_t (NULL = the
+ *     device's null stream).  Nothing synchronises unless the entry point
+ *     says so.
+ *   - Every call returns BLT_OK (0) or a negative blt_status.  The message of
+ *     the last failure on the calling thread is returned by blt_last_error().
+ *     No exception or abort crosses the ABI (the reference panics on bad
+ *     shapes; the Rust binding maps a non-zero status to panic!).
+ */
+#ifndef BLT_HIP_H
+#define BLT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* blt_stream_t; /* hipStream_t */
+
+typedef enum blt_status {
+  BLT_OK = 0,
+  BLT_ERR_INVALID = -1,  /* null pointer / bad enum value */
+  BLT_ERR_SHAPE = -2,    /* shape or size outside what the op accepts */
+  BLT_ERR_HIP = -3,      /* HIP runtime error (launch, copy, device) */
+  BLT_ERR_OOM = -4,      /* device allocation failed */
+  BLT_ERR_NODEV = -5     /* no usable gfx950 device */
+} blt_status;
+
+/* RMSNorm epsilon placement (the reference has both, see fused_rms_norm). */
+typedef enum blt_eps_mode {
+  BLT_EPS_AFTER_SQRT = 0,  /* x / (sqrt(mean x^2) + eps) * w   model.rs:758-770, backend.rs:502-506 */
+  BLT_EPS_INSIDE_SQRT = 1  /* x / sqrt(mean x^2 + eps) * w     rms_norm_kernel.rs:40-43 */
+} blt_eps_mode;
+
+/* Boundary rule for blt_patch_boundaries. */
+typedef enum blt_patch_mode {
+  BLT_PATCH_MONOTONIC = 0, /* m[0]=m[1]=1, m[t] = (H[t]-H[t-1]) > thr   patcher.rs:80-118 */
+  BLT_PATCH_GLOBAL = 1     /* m[0]=m[1]=1, m[t] = H[t] > thr (build-defined layout, same specials) */
+} blt_patch_mode;
+
+/* Library-level --------------------------------------------------------- */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* blt_last_error(void);
+/* Library version string. */
+const char* blt_version(void);
+/* Number of visible gfx950 devices (0 when there is no GPU); never fails. */
+int blt_device_count(void);
+/* Wait for all work queued on `stream`. */
+int blt_stream_sync(blt_stream_t stream);
+
+/* Fused ops: trait FusedOpsBackend (src/fused_ops/mod.rs:58-145) -------- */
+
+/* fused_entropy (mod.rs:62, wrapper mod.rs:155-159; NdArray form patcher.rs:38-63).
+ * logits [rows, vocab] f32 -> out [rows] f32, H = -sum softmax*log_softmax, natural log. */
+int blt_fused_entropy_f32(const float* logits, float* out, int64_t rows, int32_t vocab,
+                          blt_stream_t stream);
+/* Same over bf16 logits (entropy accumulated in f32). */
+int blt_fused_entropy_bf16(const uint16_t* logits, float* out, int64_t rows, int32_t vocab,
+                           blt_stream_t stream);
+
+/* fused_rms_norm (mod.rs:67-73, wrapper mod.rs:162-176).
+ * x [rows, dim] -> y [rows, dim]; w [dim].  l2_out (may be NULL) receives
+ * sqrt(sum x^2) of each input row (the pre-norm embedding norm, model.rs:291-300). */
+int blt_fused_rms_norm_f32(const float* x, const float* w, float* y, float* l2_out,
+                           int64_t rows, int32_t dim, float eps, int32_t eps_mode,
+                           blt_stream_t stream);
+int blt_fused_rms_norm_bf16(const uint16_t* x, const uint16_t* w, uint16_t* y, float* l2_out,
+                            int64_t rows, int32_t dim, float eps, int32_t eps_mode,
+                            blt_stream_t stream);
+
+/* fused_softmax over the last dim (mod.rs:78, wrapper mod.rs:179-185). x,y [rows, n] f32. */
+int blt_fused_softmax_f32(const float* x, float* y, int64_t rows, int32_t n,
+                          blt_stream_t stream);
+
+/* fused_l2_norm (mod.rs:83, wrapper mod.rs:188-192). x [rows, dim] -> out [rows]. */
+int blt_fused_l2_norm_f32(const float* x, float* out, int64_t rows, int32_t dim,
+                          blt_stream_t stream);
+int blt_fused_l2_norm_bf16(const uint16_t* x, float* out, int64_t rows, int32_t dim,
+                           blt_stream_t stream);
+
+/* fused_silu_gate (mod.rs:89-92, wrapper mod.rs:195-205). out = silu(g) * u, n elements. */
+int blt_fused_silu_gate_f32(const float* g, const float* u, float* out, int64_t n,
+                            blt_stream_t stream);
+int blt_fused_silu_gate_bf16(const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t n,
+                             blt_stream_t stream);
+
+/* fused_coherence (mod.rs:97-101, wrapper mod.rs:208-220). out = n^2 / (H + eps). */
+int blt_fused_coherence_f32(const float* norms, const float* entropies, float* out,
+                            int64_t n, float eps, blt_stream_t stream);
+
+/* fused_attention (mod.rs:104-114, wrapper mod.rs:225-236) extended with RoPE and
+ * a sliding window.  q,k,v,o are bf16 [B, H, T, d] (head-major, as mod.rs:104-107)
+ * when the strides below say so; any (b,h,t) strides with unit d-stride are
+ * accepted, in elements.  Only d = 64 is supported.
+ *   causal: 1 = key j visible to query i iff j <= i (model.rs:153-165)
+ *   window: 0 = unlimited; W > 0 additionally requires j > i - W
+ *   rope_theta: 0 = no rotation; > 0 rotates q and k (half-split pairs,
+ *               model.rs:24-52,107-147) at positions t = 0..T-1 before QK^T.
+ * Softmax in f32 with scale 1/sqrt(d); QK^T and PV on bf16 MFMA, f32 accumulate.
+ * workspace: when rope_theta > 0, a device buffer of at least
+ *            blt_attention_workspace_bytes(B,H,T,d) bytes (else may be NULL). */
+int64_t blt_attention_workspace_bytes(int64_t B, int64_t H, int64_t T, int32_t d);
+int blt_fused_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                             uint16_t* o, int64_t B, int64_t H, int64_t T, int32_t d,
+                             int64_t sb_q, int64_t sh_q, int64_t st_q,
+                             int64_t sb_kv, int64_t sh_kv, int64_t st_kv,
+                             int64_t sb_o, int64_t sh_o, int64_t st_o,
+                             int32_t causal, int32_t window, float rope_theta,
+                             void* workspace, blt_stream_t stream);
+
+/* RoPE table, precompute_freqs_cis (model.rs:24-52): out [max_seqlen, head_dim/2, 2]
+ * f32 (cos, sin), computed on the host in the reference's f32 order, copied to device. */
+int blt_rope_table_f32(float* out_device, int32_t head_dim, int32_t max_seqlen, double theta,
+                       blt_stream_t stream);
+
+/* Patcher (src/patcher.rs) --------------------------------------------- */
+
+/* patch_start_mask_from_entropy_with_monotonicity (patcher.rs:80-118) fused with
+ * patch_start_indices_cpu (patcher.rs:124-142) and patch_lengths_from_start_indices
+ * (patcher.rs:144-164), done on the device.
+ *   H [B, T] f32.  Outputs (each may be NULL):
+ *   mask    [B, T] int32: 1 = patch start, else 0
+ *   starts  [B, T] int32: row b holds its count[b] start indices, ascending
+ *   lengths [B, T] int32: row b holds count[b] patch lengths (sum = T)
+ *   count   [B]    int32
+ *   mode: blt_patch_mode; thr: delta (monotonic) or theta (global), compared in f32. */
+int blt_patch_boundaries(const float* H, int64_t B, int64_t T, float thr, int32_t mode,
+                         int32_t* mask, int32_t* starts, int32_t* lengths, int32_t* count,
+                         blt_stream_t stream);
+
+/* Entropy model: LMTransformer (src/model.rs) ------------------------- */
+
+/* LMTransformerConfig (model.rs:167-180) with the derived sizes resolved. */
+typedef struct blt_model_config {
+  int32_t dim;        /* 768 */
+  int32_t n_layers;   /* 14 */
+  int32_t n_heads;    /* 12 (n_kv_heads == n_heads; head_dim = dim / n_heads = 64) */
+  int32_t ffn_hidden; /* resolved FFN width: 768 as configured (model.rs:468-473), 2048 in real weights */
+  int32_t vocab;      /* 260 */
+  int32_t max_seqlen; /* 8192: bound of the RoPE table */
+  float norm_eps;     /* 1e-5, eps after sqrt */
+  float rope_theta;   /* 10000 */
+  int32_t window;     /* 0 = full causal (reference semantics); W > 0 = sliding window */
+} blt_model_config;
+
+/* Host-side weights in the reference's layouts (Burn Linear weight is [in, out]):
+ * every pointer is host memory holding bf16 bits; the library packs them into
+ * its own device layout.  Per layer l, arrays are concatenated over layers:
+ *   tok_embeddings [vocab, dim]                                model.rs:190
+ *   attention_norm [L, dim], ffn_norm [L, dim]                 model.rs:481-498
+ *   wq, wk, wv, wo [L, dim, dim]                               model.rs:536-550
+ *   w1, w3 [L, dim, hidden], w2 [L, hidden, dim]               model.rs:704-714
+ *   norm [dim], output [dim, vocab]                            model.rs:205-212 */
+typedef struct blt_model_weights {
+  const uint16_t* tok_embeddings;
+  const uint16_t* attention_norm;
+  const uint16_t* ffn_norm;
+  const uint16_t* wq;
+  const uint16_t* wk;
+  const uint16_t* wv;
+  const uint16_t* wo;
+  const uint16_t* w1;
+  const uint16_t* w2;
+  const uint16_t* w3;
+  const uint16_t* norm;
+  const uint16_t* output;
+} blt_model_weights;
+
+/* ModelOutput (model.rs:229-245).  Device buffers owned by the caller; any may be NULL. */
+typedef struct blt_model_outputs {
+  float* logits;              /* [B, T, vocab] f32 */
+  float* pre_norm_embeddings; /* [B, T, dim] f32 */
+  float* embedding_norms;     /* [B, T] f32 */
+  float* entropies;           /* [B, T] f32 */
+  float* coherence_scores;    /* [B, T] f32, n^2 / (H + 1e-6) */
+} blt_model_outputs;
+
+typedef struct blt_model blt_model;
+
+/* LMTransformerConfig::init + load_record (model.rs:182-226, model_loader.rs:103-145).
+ * Packs the weights onto `device`.  max_tokens bounds B*T of later forwards (it
+ * sizes the workspace). */
+int blt_model_create(int32_t device, const blt_model_config* cfg, const blt_model_weights* w,
+                     int64_t max_tokens, blt_model** out);
+int blt_model_destroy(blt_model* m);
+/* Device bytes held by the model (weights + workspace). */
+int64_t blt_model_device_bytes(const blt_model* m);
+
+/* LMTransformer::forward_with_embeddings (model.rs:269-322).
+ * tokens [B, T] int32 device buffer; 1 <= T <= max_seqlen, B*T <= max_tokens. */
+int blt_model_forward(blt_model* m, const int32_t* tokens, int64_t B, int64_t T,
+                      const blt_model_outputs* out, blt_stream_t stream);
+
+/* Per-stage timing of blt_model_forward with HIP events recorded on the
+ * forward's stream between its kernels (for roofline reporting). */
+typedef enum blt_stage {
+  BLT_STAGE_EMBED = 0,
+  BLT_STAGE_RMSNORM = 1,
+  BLT_STAGE_QKV_GEMM = 2,
+  BLT_STAGE_ATTENTION = 3,
+  BLT_STAGE_O_GEMM = 4,
+  BLT_STAGE_W13_GEMM = 5,
+  BLT_STAGE_W2_GEMM = 6,
+  BLT_STAGE_FINAL_NORM = 7,
+  BLT_STAGE_HEAD_GEMM = 8,
+  BLT_STAGE_ENTROPY = 9,
+  BLT_STAGE_COHERENCE = 10,
+  BLT_NUM_STAGES = 11
+} blt_stage;
+/* on != 0: record events in later forwards. */
+int blt_model_set_profiling(blt_model* m, int32_t on);
+/* Waits for the last recorded event; writes per-stage total milliseconds and
+ * launch counts for the forwards since the previous read (n >= BLT_NUM_STAGES). */
+int blt_model_read_profile(blt_model* m, double* ms, int64_t* launches, int32_t n);
+const char* blt_stage_name(int32_t stage);
+
+/* Synthetic inputs (host memory, deterministic across C and Python) ----- */
+
+/* splitmix64-seeded N(mean, std) samples (Box-Muller in double), as f32. */
+int blt_synth_normal_f32(uint64_t seed, float* out, int64_t n, double mean, double std);
+/* Same, rounded to bf16 (round to nearest even). */
+int blt_synth_normal_bf16(uint64_t seed, uint16_t* out, int64_t n, double mean, double std);
+/* Byte tokens: Zipf(s) over the 95 printable ASCII bytes (a seeded rank
+ * permutation), a fraction `p_uniform` replaced by uniform bytes 0..255, plus
+ * `offset` (4 = tokenizer.rs OFFSET). */
+int blt_synth_tokens(uint64_t seed, int32_t* out, int64_t n, double zipf_s, double p_uniform,
+                     int32_t offset);
+
+/* Low-level: the GEMM used by the model, exposed for testing and benchmarking.
+ * C[M,N] = A[M,K] * Bt[N,K]^T, bf16 in, f32 accumulate, bf16 out.
+ * Requires K % 64 == 0, N % 64 == 0. */
+int blt_gemm_bf16(const uint16_t* A, const uint16_t* Bt, uint16_t* C, int64_t M, int64_t N,
+                  int64_t K, blt_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BLT_HIP_H */

@@ -1,0 +1,214 @@
+"""CPU oracle for the entropy-patching path (TEST INFRASTRUCTURE ONLY).
+
+ctypes bindings to liboracle.so (oracle.c, a C restatement of blt-burn's
+NdArray path).  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg use this package, always as the checker.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+
+
+def build():
+    """Compile liboracle.so with the Makefile beside this file."""
+    subprocess.run(["make", "-s", "-C", HERE, "-B", "liboracle.so"], check=True)
+    return LIB_PATH
+
+
+class Cfg(ctypes.Structure):
+    _fields_ = [("dim", _i32), ("n_layers", _i32), ("n_heads", _i32), ("hidden", _i32),
+                ("vocab", _i32), ("max_seqlen", _i32), ("norm_eps", ctypes.c_float),
+                ("rope_theta", ctypes.c_float), ("window", _i32)]
+
+
+class Weights(ctypes.Structure):
+    _fields_ = [(n, _f32p) for n in
+                ("emb", "attn_norm", "ffn_norm", "wq", "wk", "wv", "wo", "w1", "w2", "w3",
+                 "norm", "out")]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        L.oracle_entropy.argtypes = [_f32p, _f32p, _i64, _i32]
+        L.oracle_rms_norm.argtypes = [_f32p, _f32p, _f32p, _i64, _i32, ctypes.c_float, _i32]
+        L.oracle_l2_norm.argtypes = [_f32p, _f32p, _i64, _i32]
+        L.oracle_softmax.argtypes = [_f32p, _f32p, _i64, _i32]
+        L.oracle_silu_gate.argtypes = [_f32p, _f32p, _f32p, _i64]
+        L.oracle_coherence.argtypes = [_f32p, _f32p, _f32p, _i64, ctypes.c_float]
+        L.oracle_patch_mask.argtypes = [_f32p, _i64, _i64, ctypes.c_float, _i32, _i32p]
+        L.oracle_patch_indices.argtypes = [_i32p, _i64, _i64, _i32p, _i32p]
+        L.oracle_patch_lengths.argtypes = [_i32p, _i32p, _i64, _i64, _i32p]
+        L.oracle_rope_table.argtypes = [_f32p, _i32, _i32, ctypes.c_double]
+        L.oracle_attention.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i32, _i32,
+                                       _i32, ctypes.c_double]
+        L.oracle_model_forward.argtypes = [ctypes.POINTER(Cfg), ctypes.POINTER(Weights), _i32p,
+                                           _i64, _i64, _f32p, _f32p, _f32p, _f32p, _f32p]
+        for f in ("oracle_entropy", "oracle_rms_norm", "oracle_l2_norm", "oracle_softmax",
+                  "oracle_silu_gate", "oracle_coherence", "oracle_patch_mask",
+                  "oracle_patch_indices", "oracle_patch_lengths", "oracle_rope_table",
+                  "oracle_attention", "oracle_model_forward"):
+            getattr(L, f).restype = None
+        _lib = L
+    return _lib
+
+
+def _f(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a, a.ctypes.data_as(_f32p)
+
+
+def _i(a):
+    a = np.ascontiguousarray(a, dtype=np.int32)
+    return a, a.ctypes.data_as(_i32p)
+
+
+def entropy(logits):
+    """[..., V] f32 -> [...] (patcher.rs:38-63)."""
+    x, px = _f(logits)
+    V = x.shape[-1]
+    out = np.empty(x.shape[:-1], np.float32)
+    lib().oracle_entropy(px, out.ctypes.data_as(_f32p), x.size // V if V else 0, V)
+    return out
+
+
+def rms_norm(x, w, eps, mode=0):
+    x, px = _f(x)
+    w, pw = _f(w)
+    D = x.shape[-1]
+    y = np.empty_like(x)
+    lib().oracle_rms_norm(px, pw, y.ctypes.data_as(_f32p), x.size // D, D, eps, mode)
+    return y
+
+
+def l2_norm(x):
+    x, px = _f(x)
+    D = x.shape[-1]
+    out = np.empty(x.shape[:-1], np.float32)
+    lib().oracle_l2_norm(px, out.ctypes.data_as(_f32p), x.size // D, D)
+    return out
+
+
+def softmax(x):
+    x, px = _f(x)
+    N = x.shape[-1]
+    y = np.empty_like(x)
+    lib().oracle_softmax(px, y.ctypes.data_as(_f32p), x.size // N, N)
+    return y
+
+
+def silu_gate(g, u):
+    g, pg = _f(g)
+    u, pu = _f(u)
+    out = np.empty_like(g)
+    lib().oracle_silu_gate(pg, pu, out.ctypes.data_as(_f32p), g.size)
+    return out
+
+
+def coherence(n, H, eps):
+    n, pn = _f(n)
+    H, pH = _f(H)
+    out = np.empty_like(n)
+    lib().oracle_coherence(pn, pH, out.ctypes.data_as(_f32p), n.size, eps)
+    return out
+
+
+def patch_mask(H, thr, mode=0):
+    """[B, T] f32 -> [B, T] int32 (patcher.rs:80-118; mode 1 = global H > thr)."""
+    H, pH = _f(H)
+    B, T = H.shape
+    m = np.zeros((B, T), np.int32)
+    lib().oracle_patch_mask(pH, B, T, thr, mode, m.ctypes.data_as(_i32p))
+    return m
+
+
+def patch_indices(mask):
+    """[B, T] int32 -> list of per-row start lists (patcher.rs:124-142)."""
+    mask, pm = _i(mask)
+    B, T = mask.shape
+    starts = np.zeros((B, T), np.int32)
+    counts = np.zeros(B, np.int32)
+    lib().oracle_patch_indices(pm, B, T, starts.ctypes.data_as(_i32p), counts.ctypes.data_as(_i32p))
+    return [starts[b, :counts[b]].tolist() for b in range(B)]
+
+
+def patch_lengths(starts, seq_len):
+    """per-row start lists -> per-row length lists (patcher.rs:144-164)."""
+    B = len(starts)
+    T = max(seq_len, 1)
+    st = np.zeros((B, T), np.int32)
+    counts = np.array([len(s) for s in starts], np.int32)
+    for b, s in enumerate(starts):
+        st[b, :len(s)] = s
+    ln = np.zeros((B, T), np.int32)
+    lib().oracle_patch_lengths(st.ctypes.data_as(_i32p), counts.ctypes.data_as(_i32p), B, seq_len,
+                               ln.ctypes.data_as(_i32p))
+    return [ln[b, :counts[b]].tolist() for b in range(B)]
+
+
+def rope_table(head_dim, max_seqlen, theta):
+    out = np.empty((max_seqlen, head_dim // 2, 2), np.float32)
+    lib().oracle_rope_table(out.ctypes.data_as(_f32p), head_dim, max_seqlen, theta)
+    return out
+
+
+def attention(q, k, v, causal=True, window=0, rope_theta=0.0):
+    """q, k, v f32 [B, H, T, d] -> o [B, H, T, d]."""
+    q, pq = _f(q)
+    k, pk = _f(k)
+    v, pv = _f(v)
+    B, H, T, d = q.shape
+    o = np.empty_like(q)
+    lib().oracle_attention(pq, pk, pv, o.ctypes.data_as(_f32p), B, H, T, d, int(causal),
+                           window, rope_theta)
+    return o
+
+
+WEIGHT_NAMES = ("emb", "attn_norm", "ffn_norm", "wq", "wk", "wv", "wo", "w1", "w2", "w3", "norm",
+                "out")
+
+
+def model_forward(cfg, weights, tokens):
+    """cfg: dict(dim, n_layers, n_heads, hidden, vocab, max_seqlen, norm_eps, rope_theta, window);
+    weights: dict of f32 arrays in the reference layouts (see oracle.c); tokens [B, T] int.
+    Returns dict(logits, pre_norm_embeddings, embedding_norms, entropies, coherence_scores)."""
+    tokens, pt = _i(tokens)
+    B, T = tokens.shape
+    c = Cfg(cfg["dim"], cfg["n_layers"], cfg["n_heads"], cfg["hidden"], cfg["vocab"],
+            cfg["max_seqlen"], cfg["norm_eps"], cfg["rope_theta"], cfg.get("window", 0))
+    keep = []
+    ptrs = []
+    for n in WEIGHT_NAMES:
+        a, p = _f(weights[n])
+        keep.append(a)
+        ptrs.append(p)
+    w = Weights(*ptrs)
+    D, V = cfg["dim"], cfg["vocab"]
+    out = {
+        "logits": np.empty((B, T, V), np.float32),
+        "pre_norm_embeddings": np.empty((B, T, D), np.float32),
+        "embedding_norms": np.empty((B, T), np.float32),
+        "entropies": np.empty((B, T), np.float32),
+        "coherence_scores": np.empty((B, T), np.float32),
+    }
+    lib().oracle_model_forward(ctypes.byref(c), ctypes.byref(w), pt, B, T,
+                               *[out[k].ctypes.data_as(_f32p) for k in
+                                 ("logits", "pre_norm_embeddings", "embedding_norms",
+                                  "entropies", "coherence_scores")])
+    return out

@@ -1,0 +1,100 @@
+"""Independent float64 NumPy statement of the reference's math, written from
+the mathematics (materialised masks and score matrices, closed-form RoPE) to
+pin the C oracle.  Test-only."""
+import numpy as np
+
+
+def entropy(logits):
+    x = np.asarray(logits, np.float64)
+    z = x - x.max(-1, keepdims=True)
+    p = np.exp(z)
+    p /= p.sum(-1, keepdims=True)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        t = np.where(p > 0, p * np.log(p), 0.0)
+    return -t.sum(-1)
+
+
+def rms_norm(x, w, eps, mode=0):
+    x = np.asarray(x, np.float64)
+    rms2 = (x * x).mean(-1, keepdims=True)
+    den = np.sqrt(rms2) + eps if mode == 0 else np.sqrt(rms2 + eps)
+    return x / den * np.asarray(w, np.float64)
+
+
+def l2_norm(x):
+    x = np.asarray(x, np.float64)
+    return np.sqrt((x * x).sum(-1))
+
+
+def softmax(x):
+    x = np.asarray(x, np.float64)
+    e = np.exp(x - x.max(-1, keepdims=True))
+    return e / e.sum(-1, keepdims=True)
+
+
+def silu_gate(g, u):
+    g = np.asarray(g, np.float64)
+    return g / (1.0 + np.exp(-g)) * np.asarray(u, np.float64)
+
+
+def rope_angles(d, T, theta):
+    i = np.arange(d // 2, dtype=np.float64)
+    inv = theta ** (-2.0 * i / d)
+    return np.arange(T, dtype=np.float64)[:, None] * inv[None, :]
+
+
+def rotate(x, theta):
+    """x [..., T, d] rotated with half-split pairs (x[m], x[m + d/2])."""
+    x = np.asarray(x, np.float64)
+    T, d = x.shape[-2], x.shape[-1]
+    a = rope_angles(d, T, theta)
+    c, s = np.cos(a), np.sin(a)
+    x1, x2 = x[..., : d // 2], x[..., d // 2:]
+    return np.concatenate([x1 * c - x2 * s, x1 * s + x2 * c], -1)
+
+
+def mask_matrix(T, causal, window):
+    i = np.arange(T)[:, None]
+    j = np.arange(T)[None, :]
+    vis = np.ones((T, T), bool)
+    if causal:
+        vis &= j <= i
+        if window > 0:
+            vis &= j > i - window
+    return np.where(vis, 0.0, -np.inf)
+
+
+def attention(q, k, v, causal=True, window=0, rope_theta=0.0):
+    """[B, H, T, d] float64, materialised [T, T] scores."""
+    q, k, v = (np.asarray(t, np.float64) for t in (q, k, v))
+    if rope_theta > 0:
+        q, k = rotate(q, rope_theta), rotate(k, rope_theta)
+    d = q.shape[-1]
+    s = q @ np.swapaxes(k, -1, -2) / np.sqrt(d) + mask_matrix(q.shape[-2], causal, window)
+    return softmax(s) @ v
+
+
+def model_forward(cfg, w, tokens):
+    """cfg dict as oracle.model_forward; w: dict of float arrays in reference layouts."""
+    D, L, Hn, F = cfg["dim"], cfg["n_layers"], cfg["n_heads"], cfg["hidden"]
+    hd = D // Hn
+    eps, theta, window = cfg["norm_eps"], cfg["rope_theta"], cfg.get("window", 0)
+    W = {k: np.asarray(v, np.float64) for k, v in w.items()}
+    tokens = np.asarray(tokens)
+    B, T = tokens.shape
+    x = W["emb"][tokens]
+    for l in range(L):
+        a = rms_norm(x, W["attn_norm"][l], eps)
+        q = (a @ W["wq"][l]).reshape(B, T, Hn, hd).transpose(0, 2, 1, 3)
+        k = (a @ W["wk"][l]).reshape(B, T, Hn, hd).transpose(0, 2, 1, 3)
+        v = (a @ W["wv"][l]).reshape(B, T, Hn, hd).transpose(0, 2, 1, 3)
+        o = attention(q, k, v, True, window, theta).transpose(0, 2, 1, 3).reshape(B, T, D)
+        x = x + o @ W["wo"][l]
+        f = rms_norm(x, W["ffn_norm"][l], eps)
+        x = x + silu_gate(f @ W["w1"][l], f @ W["w3"][l]) @ W["w2"][l]
+    pre = x
+    norms = l2_norm(x)
+    logits = rms_norm(x, W["norm"], eps) @ W["out"]
+    H = entropy(logits)
+    return {"logits": logits, "pre_norm_embeddings": pre, "embedding_norms": norms,
+            "entropies": H, "coherence_scores": norms ** 2 / (H + 1e-6)}

@@ -1,0 +1,104 @@
+"""Parity of the whole entropy-model forward (blt_model_forward) with the CPU
+oracle on identical seeded bf16 weights and tokens.  Tolerances (BASELINE):
+entropies 2e-2 abs, pre-norm embedding norms 1e-2 rel, boundaries bit-exact
+on the same entropies.  At the full B=16 x 8192 size, size-independent
+properties instead: per-row independence and causal prefix consistency."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from blt_burn_amd import model as M
+from blt_burn_amd import patcher, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_weights(w):
+    f = {k: synth.bf16_to_f32(v) for k, v in w.items()}
+    return {"emb": f["tok_embeddings"], "attn_norm": f["attention_norm"],
+            "ffn_norm": f["ffn_norm"], "wq": f["wq"], "wk": f["wk"], "wv": f["wv"],
+            "wo": f["wo"], "w1": f["w1"], "w2": f["w2"], "w3": f["w3"], "norm": f["norm"],
+            "out": f["output"]}
+
+
+def _run(cfg, hidden, B, T, window, seed):
+    w = M.random_weights(cfg, seed, hidden=hidden)
+    tok = synth.tokens(synth.config_seed(4) + seed, (B, T))
+    m = M.LMTransformer(cfg, w, device=0, max_tokens=B * T, window=window)
+    out = m.forward_with_embeddings(torch.from_numpy(tok).cuda())
+    torch.cuda.synchronize()
+    ref = oracle.model_forward(dict(dim=cfg.dim, n_layers=cfg.n_layers,
+                                    n_heads=cfg.resolved_n_heads(), hidden=hidden,
+                                    vocab=cfg.vocab_size, max_seqlen=cfg.max_seqlen,
+                                    norm_eps=cfg.norm_eps, rope_theta=cfg.rope_theta,
+                                    window=window), _oracle_weights(w), tok)
+    return out, ref
+
+
+def _compare(out, ref, label):
+    H = out.entropies.cpu().numpy()
+    n = out.embedding_norms.cpu().numpy()
+    pre = out.pre_norm_embeddings.cpu().numpy()
+    dH = np.abs(H - ref["entropies"]).max()
+    dn = (np.abs(n - ref["embedding_norms"]) / ref["embedding_norms"]).max()
+    dpre = np.abs(pre - ref["pre_norm_embeddings"]).max() / np.abs(ref["pre_norm_embeddings"]).max()
+    dl = np.abs(out.logits.cpu().numpy() - ref["logits"]).max()
+    print("%s: entropy max|d|=%.2e norms max rel=%.2e pre max rel=%.2e logits max|d|=%.2e"
+          % (label, dH, dn, dpre, dl))
+    assert dH < 2e-2 and dn < 1e-2, (dH, dn)
+    np.testing.assert_allclose(out.coherence_scores.cpu().numpy(), ref["coherence_scores"],
+                               rtol=3e-2)
+    # boundaries: bit-exact given the same entropy array
+    for mode, thr in ((patcher.PATCH_MONOTONIC, 0.2), (patcher.PATCH_GLOBAL, 1.33)):
+        mask = patcher.patch_boundaries(out.entropies, thr, mode)[0].cpu().numpy()
+        np.testing.assert_array_equal(mask, oracle.patch_mask(H, thr, mode))
+
+
+@pytest.mark.parametrize("window", [0, 32])
+def test_tiny_model(window):
+    cfg = M.LMTransformerConfig(dim=128, n_layers=2, n_heads=2, ffn_dim_multiplier=2.0,
+                                multiple_of=64, max_seqlen=512, vocab_size=260)
+    out, ref = _run(cfg, 256, 2, 200, window, seed=3)
+    _compare(out, ref, "tiny w=%d" % window)
+
+
+@pytest.mark.parametrize("window,T", [(0, 256), (512, 700)])
+def test_entropy_model_dims(window, T):
+    # the BLT entropy model at real size (14 x 768, 12 heads, FFN 2048, V 260), short T
+    cfg = M.entropy_model_config()
+    out, ref = _run(cfg, 2048, 1, T, window, seed=4)
+    _compare(out, ref, "entropy-model T=%d w=%d" % (T, window))
+
+
+def test_reference_configured_ffn_768():
+    # LMTransformerConfig::init as configured gives FFN 768 (model.rs:468-473)
+    cfg = M.entropy_model_config()
+    cfg.n_layers = 2
+    out, ref = _run(cfg, cfg.ffn_hidden(), 2, 128, 0, seed=5)
+    _compare(out, ref, "ffn768")
+
+
+def test_full_size_properties():
+    # config 4 size: B=16, T=8192, window 512.  Rows are independent and the
+    # forward is causal: row b of the batch equals that sequence run alone, and
+    # a prefix run gives the prefix of the outputs (bit-exact).
+    cfg = M.entropy_model_config()
+    w = M.random_weights(cfg, 11, hidden=2048)
+    B, T = 16, 8192
+    tok = torch.from_numpy(synth.tokens(synth.config_seed(4), (B, T))).cuda()
+    m = M.LMTransformer(cfg, w, device=0, max_tokens=B * T, window=512)
+    out = m.forward_with_embeddings(tok)
+    H = out.entropies
+    assert torch.isfinite(H).all() and (H >= 0).all() and (H <= np.log(260) + 1e-4).all()
+    assert torch.isfinite(out.pre_norm_embeddings).all()
+    one = m.forward_with_embeddings(tok[5:6].contiguous())
+    assert torch.equal(one.entropies[0], H[5])
+    assert torch.equal(one.embedding_norms[0], out.embedding_norms[5])
+    pre = m.forward_with_embeddings(tok[2:3, :3000].contiguous())
+    assert torch.equal(pre.entropies[0], H[2, :3000])
+    _, starts, lengths, counts = patcher.patch_boundaries(H, 0.2, patcher.PATCH_MONOTONIC)
+    c = counts.cpu()
+    ln = lengths.cpu()
+    for b in range(B):
+        assert int(ln[b, :c[b]].sum()) == T

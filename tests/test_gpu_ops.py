@@ -1,0 +1,226 @@
+"""Parity of the gfx950 fused ops and patcher kernels with the CPU oracle
+(bit-exact for boundaries/indices; tolerances stated per test), on the
+reference tests' shapes and on BASELINE config 1/2/3 shapes."""
+import ctypes
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from blt_burn_amd import fused_ops as F
+from blt_burn_amd import patcher, synth
+from blt_burn_amd import _lib
+
+pytestmark = pytest.mark.gpu
+KAT = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "kat.json")))
+DEV = "cuda:0"
+
+
+def cuda(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def bf16(a):
+    """f32 numpy -> (bf16 cuda tensor, the same values as f32 numpy)."""
+    t = cuda(a.astype(np.float32)).to(torch.bfloat16)
+    return t, t.float().cpu().numpy()
+
+
+# ---------------------------------------------------------------- entropy
+@pytest.mark.parametrize("case", KAT["entropy"], ids=lambda c: c["name"])
+def test_entropy_kat(case):
+    x = np.full(case["shape"], case["fill"], np.float32)
+    if "hot" in case:
+        x[..., 0] = case["hot"]
+    H = F.fused_entropy(cuda(x), x.shape[-1]).cpu().numpy()
+    assert H.shape == tuple(case["shape"][:-1])
+    assert np.all(np.abs(H - case["expected"]) < case["tol"])
+
+
+@pytest.mark.parametrize("shape,std,mean", [((2, 4, 10), 1.0, 0.0), ((2, 128, 260), 1.0, 0.0),
+                                            ((1, 32, 260), 1.0, 0.0), ((4, 1, 260), 1.0, 0.0),
+                                            ((1, 64, 260), 20.0, 50.0), ((3, 5, 1000), 2.0, 0.0),
+                                            ((2, 7, 3000), 2.0, 0.0), ((2, 9, 97), 2.0, 0.0)])
+def test_entropy_vs_oracle(shape, std, mean):
+    x = synth.normal_f32(11, shape, mean, std)
+    H = F.fused_entropy(cuda(x), shape[-1]).cpu().numpy()
+    ref = oracle.entropy(x)
+    assert np.all(np.isfinite(H)) and np.all(H >= -1e-6)
+    np.testing.assert_allclose(H, ref, atol=1e-4)  # reference tests: 1e-4 / 1e-3
+
+
+def test_entropy_config1_full_size():
+    # logits f32 [4, 8192, 260] ~ N(0, 2)
+    x = synth.normal_f32(synth.config_seed(1), (4, 8192, 260), 0.0, 2.0)
+    H = F.fused_entropy(cuda(x), 260).cpu().numpy()
+    np.testing.assert_allclose(H, oracle.entropy(x), atol=1e-4)
+
+
+def test_entropy_bf16():
+    xb, xf = bf16(synth.normal_f32(12, (8, 64, 260), 0.0, 2.0))
+    H = F.fused_entropy(xb, 260).cpu().numpy()
+    np.testing.assert_allclose(H, oracle.entropy(xf), atol=1e-4)
+
+
+# ---------------------------------------------------------------- norms / elementwise
+@pytest.mark.parametrize("mode", [F.EPS_AFTER_SQRT, F.EPS_INSIDE_SQRT])
+@pytest.mark.parametrize("dim", [64, 768, 1000, 4100])
+def test_rms_norm_f32(mode, dim):
+    x = synth.normal_f32(13, (2, 8, dim))
+    w = synth.normal_f32(14, dim, 1.0, 0.2)
+    l2 = torch.empty((2, 8), dtype=torch.float32, device=DEV)
+    y = F.fused_rms_norm(cuda(x), cuda(w), 1e-6, mode, l2_out=l2).cpu().numpy()
+    np.testing.assert_allclose(y, oracle.rms_norm(x, w, 1e-6, mode), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(l2.cpu().numpy(), oracle.l2_norm(x), rtol=1e-5)
+
+
+def test_rms_norm_bf16_config2():
+    # x [32768, 768] ~ N(0,1), w ~ 1 + N(0, 0.02), eps 1e-5, bf16
+    xb, xf = bf16(synth.normal_f32(synth.config_seed(2), (1, 32768, 768)))
+    wb, wf = bf16(synth.normal_f32(synth.config_seed(2) + 1, 768, 1.0, 0.02))
+    l2 = torch.empty((1, 32768), dtype=torch.float32, device=DEV)
+    y = F.fused_rms_norm(xb, wb, 1e-5, F.EPS_AFTER_SQRT, l2_out=l2).float().cpu().numpy()
+    ref = oracle.rms_norm(xf, wf, 1e-5, 0)
+    # bf16 output: within one bf16 rounding (2^-8 relative) of the f32 oracle
+    np.testing.assert_allclose(y, ref, rtol=2 ** -8, atol=1e-6)
+    np.testing.assert_allclose(l2.cpu().numpy(), oracle.l2_norm(xf), rtol=1e-5)
+
+
+def test_l2_norm():
+    x = synth.normal_f32(15, (2, 16, 128))  # test_fused_ops.rs:63-94
+    np.testing.assert_allclose(F.fused_l2_norm(cuda(x)).cpu().numpy(), oracle.l2_norm(x),
+                               atol=1e-4)
+    xb, xf = bf16(x)
+    np.testing.assert_allclose(F.fused_l2_norm(xb).cpu().numpy(), oracle.l2_norm(xf), rtol=1e-5)
+
+
+@pytest.mark.parametrize("shape", [(2, 8, 64), (2, 8, 32, 32), (3, 300), (2, 2, 5000)])
+def test_softmax(shape):
+    x = synth.normal_f32(16, shape)
+    y = F.fused_softmax(cuda(x), shape[-1]).cpu().numpy()
+    np.testing.assert_allclose(y, oracle.softmax(x), atol=1e-6)
+    big = synth.normal_f32(17, (2, 8, 64), 50.0, 20.0)  # test_fused_ops.rs:269-287
+    yb = F.fused_softmax(cuda(big), 64).cpu().numpy()
+    assert np.all(np.isfinite(yb)) and np.all((yb >= 0) & (yb <= 1))
+
+
+@pytest.mark.parametrize("n", [(2, 8, 256), (1, 16, 128), (3, 5, 7)])
+def test_silu_gate(n):
+    g, u = synth.normal_f32(18, n), synth.normal_f32(19, n)
+    np.testing.assert_allclose(F.fused_silu_gate(cuda(g), cuda(u)).cpu().numpy(),
+                               oracle.silu_gate(g, u), atol=1e-5)
+    gb, gf = bf16(g)
+    ub, uf = bf16(u)
+    got = F.fused_silu_gate(gb, ub).float().cpu().numpy()
+    np.testing.assert_allclose(got, oracle.silu_gate(gf, uf), rtol=2 ** -8, atol=1e-6)
+
+
+def test_silu_gate_bf16_config2():
+    gb, gf = bf16(synth.normal_f32(synth.config_seed(2) + 2, (32768, 2048)))
+    ub, uf = bf16(synth.normal_f32(synth.config_seed(2) + 3, (32768, 2048)))
+    got = F.fused_silu_gate(gb, ub).float().cpu().numpy()
+    np.testing.assert_allclose(got, oracle.silu_gate(gf, uf), rtol=2 ** -8, atol=1e-6)
+
+
+def test_coherence():
+    n = synth.normal_f32(20, (4, 32), 5.0, 2.0)
+    H = np.abs(synth.normal_f32(21, (4, 32), 2.5, 1.0)) + 0.1
+    np.testing.assert_allclose(F.fused_coherence(cuda(n), cuda(H), 1e-6).cpu().numpy(),
+                               oracle.coherence(n, H, 1e-6), rtol=1e-5)
+
+
+# ---------------------------------------------------------------- patch boundaries
+def _check_boundaries(H, thr, mode):
+    mask, starts, lengths, counts = patcher.patch_boundaries(cuda(H), thr, mode)
+    ref_mask = oracle.patch_mask(H, thr, mode)
+    np.testing.assert_array_equal(mask.cpu().numpy(), ref_mask)
+    ref_starts = oracle.patch_indices(ref_mask)
+    ref_len = oracle.patch_lengths(ref_starts, H.shape[1])
+    c = counts.cpu().numpy()
+    st, ln = starts.cpu().numpy(), lengths.cpu().numpy()
+    for b in range(H.shape[0]):
+        assert c[b] == len(ref_starts[b])
+        assert st[b, :c[b]].tolist() == ref_starts[b]
+        assert ln[b, :c[b]].tolist() == ref_len[b]
+        assert int(ln[b, :c[b]].sum()) == H.shape[1]
+
+
+@pytest.mark.parametrize("case", KAT["patch"], ids=lambda c: c["name"])
+def test_patch_kat(case):
+    H = np.array(case["H"], np.float32)
+    mode = patcher.PATCH_MONOTONIC if case["mode"] == "monotonic" else patcher.PATCH_GLOBAL
+    mask, starts, lengths, counts = patcher.patch_boundaries(cuda(H), case["thr"], mode)
+    assert mask.cpu().tolist() == case["mask"]
+    c = counts.cpu().tolist()
+    assert [starts[b, :c[b]].cpu().tolist() for b in range(len(c))] == case["starts"]
+    assert [lengths[b, :c[b]].cpu().tolist() for b in range(len(c))] == case["lengths"]
+
+
+@pytest.mark.parametrize("B,T", [(1, 0), (3, 1), (2, 2), (2, 3), (4, 8191), (4, 8192), (2, 8193),
+                                 (1, 20000), (16, 8192)])
+@pytest.mark.parametrize("mode,thr", [(0, 0.2), (1, 1.33), (0, 1.335)])
+def test_patch_boundaries_vs_oracle(B, T, mode, thr):
+    H = np.abs(synth.normal_f32(22 + T, (B, T), 1.4, 0.6))
+    _check_boundaries(H, thr, mode)
+
+
+def test_patch_boundaries_config1():
+    # config 1: entropies of N(0, 2) logits; global (1.33) and monotonic (0.2) masks
+    x = synth.normal_f32(synth.config_seed(1), (4, 8192, 260), 0.0, 2.0)
+    Hd = F.fused_entropy(cuda(x), 260)
+    H = Hd.cpu().numpy()
+    _check_boundaries(H, 1.33, 1)
+    _check_boundaries(H, 0.2, 0)
+    # shifted-logit variant: scale rows so entropies straddle the global threshold
+    xs = x * np.linspace(0.2, 4.0, 8192, dtype=np.float32)[None, :, None]
+    Hs = F.fused_entropy(cuda(xs), 260).cpu().numpy()
+    assert 0.05 < (Hs > 1.33).mean() < 0.95
+    _check_boundaries(Hs, 1.33, 1)
+    _check_boundaries(Hs, 0.2, 0)
+    # mask API of the reference
+    m = patcher.patch_start_mask_from_entropy_with_monotonicity(Hd, 0.2).cpu().numpy()
+    np.testing.assert_array_equal(m, oracle.patch_mask(H, 0.2, 0))
+
+
+# ---------------------------------------------------------------- GEMM and attention
+@pytest.mark.parametrize("M,N,K", [(256, 256, 64), (1000, 320, 768), (4096, 2304, 768),
+                                   (131072 // 8, 768, 2048)])
+def test_gemm_vs_torch_fp32(M, N, K):
+    a = torch.randn(M, K, device=DEV).to(torch.bfloat16)
+    b = torch.randn(N, K, device=DEV).to(torch.bfloat16)
+    c = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+    _lib.check(_lib.lib().blt_gemm_bf16(a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K,
+                                        torch.cuda.current_stream().cuda_stream), "gemm")
+    ref = a.float() @ b.float().t()
+    err = (c.float() - ref).abs().max().item()
+    assert err <= 2 ** -7 * ref.abs().max().item() + 1e-2, err
+
+
+def _attn_case(B, H, T, causal, window, theta, seed=30):
+    q, k, v = (synth.normal_f32(seed + i, (B, H, T, 64)) for i in range(3))
+    qb, qf = bf16(q)
+    kb, kf = bf16(k)
+    vb, vf = bf16(v)
+    o = F.fused_attention(qb, kb, vb, causal, window=window, rope_theta=theta).float().cpu().numpy()
+    ref = oracle.attention(qf, kf, vf, causal, window, theta)
+    return o, ref
+
+
+@pytest.mark.parametrize("B,H,T,causal,window,theta", [
+    (1, 2, 64, True, 0, 0.0), (2, 3, 200, True, 0, 0.0), (1, 2, 333, True, 64, 0.0),
+    (1, 1, 130, False, 0, 0.0), (1, 2, 300, True, 0, 10000.0), (2, 2, 700, True, 512, 10000.0),
+    (1, 1, 1, True, 0, 10000.0), (1, 1, 97, True, 1, 0.0)])
+def test_attention_vs_oracle(B, H, T, causal, window, theta):
+    o, ref = _attn_case(B, H, T, causal, window, theta)
+    # bf16 operands and bf16 P in the PV product: |err| <= 2e-2 for N(0,1) inputs
+    np.testing.assert_allclose(o, ref, atol=2e-2, rtol=0)
+
+
+def test_attention_config3_b1():
+    # config 3 shape at B=1 (the CPU comparison size): T=4096, 12 heads, window 512, RoPE
+    o, ref = _attn_case(1, 12, 4096, True, 512, 10000.0, seed=synth.config_seed(3))
+    np.testing.assert_allclose(o, ref, atol=2e-2, rtol=0)
