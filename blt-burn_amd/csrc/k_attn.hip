@@ -31,7 +31,9 @@ constexpr int K_TILE = BKV * D;
 constexpr int V_TILE = D * VT_LD;
 constexpr int STAGE = K_TILE + V_TILE;
 
-__device__ inline int kswz(int key, int chunk) { return key * D + ((chunk ^ (key & 7)) << 3); }
+// K rows are 128 B: chunk c of key row k is stored at c ^ ((k >> 1) & 7), so the
+// 16 rows one LDS cycle serves for an operand load fall in 16 distinct banks.
+__device__ inline int kswz(int key, int chunk) { return key * D + ((chunk ^ ((key >> 1) & 7)) << 3); }
 
 __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
