@@ -44,6 +44,94 @@ def stage_flops(stage, M, B, T, D, F, V, H, window):
     }.get(stage)
 
 
+STAGE_OF_GEMM = ("qkv_gemm_rope", "o_gemm_residual", "w13_gemm_silu", "w2_gemm_residual")
+
+
+def _dispatch_stages(names, layers):
+    """Map the kernel names of one forward's dispatches, in order, to model stages."""
+    out, g = [], 0
+    for n in names:
+        if "gemm_bf16_kernel" in n:
+            out.append(STAGE_OF_GEMM[g % 4] if g < 4 * layers else "head_gemm")
+            g += 1
+        elif "attn_fwd_kernel" in n:
+            out.append("attention")
+        elif "rmsnorm" in n:
+            out.append("rmsnorm")
+        elif "entropy_kernel" in n:
+            out.append("entropy")
+        elif "patch_boundary_kernel" in n:
+            out.append("patch_boundaries")
+        elif "embed_kernel" in n:
+            out.append("embed")
+        elif "coherence_kernel" in n:
+            out.append("coherence")
+        else:
+            out.append(None)
+    return out
+
+
+def _read_counter_csv(path, counter):
+    import csv
+    rows = [r for r in csv.DictReader(open(path)) if r["Counter_Name"] == counter]
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    return [(r["Kernel_Name"], float(r["Counter_Value"])) for r in rows]
+
+
+def summarize(args):
+    """Per-stage HBM traffic per launch from rocprofv3 --pmc runs of
+    `bench.py --steps 1 --warmup 0 --no-cpu` (FETCH_SIZE and WRITE_SIZE, KiB per
+    dispatch), each scaled by the bytes a copy of --copy-bytes reads/writes
+    divided by what the counter reports for that copy.  Prints JSON."""
+    import glob
+    find = lambda d: glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)[0]
+    fetch = _read_counter_csv(find(args.summarize[0]), "FETCH_SIZE")
+    write = _read_counter_csv(find(args.summarize[1]), "WRITE_SIZE")
+    cf = max(v for _, v in _read_counter_csv(find(args.summarize[2]), "FETCH_SIZE"))
+    cw = max(v for _, v in _read_counter_csv(find(args.summarize[3]), "WRITE_SIZE"))
+    kf, kw = args.copy_bytes / (cf * 1024.0), args.copy_bytes / (cw * 1024.0)
+    L = 14
+    res = {"fetch_scale": kf, "write_scale": kw, "copy_bytes": args.copy_bytes,
+           "copy_fetch_kib": cf, "copy_write_kib": cw, "stages": {}}
+    for lst, key, k in ((fetch, "fetch_bytes", kf), (write, "write_bytes", kw)):
+        ours = [(n, v) for n, v in lst if "blt::" in n]
+        for st, (n, v) in zip(_dispatch_stages([n for n, _ in ours], L), ours):
+            if st is None:
+                continue
+            d = res["stages"].setdefault(st, {"launches": 0})
+            d[key] = d.get(key, 0.0) + v * 1024.0 * k
+            if key == "fetch_bytes":
+                d["launches"] += 1
+    for d in res["stages"].values():
+        for key in ("fetch_bytes", "write_bytes"):
+            d[key] = round(d.get(key, 0.0) / max(d["launches"], 1))
+    print(json.dumps(res, indent=1))
+
+
+def summarize_trace(path):
+    """Per-stage mean kernel duration from a rocprofv3 --kernel-trace CSV of
+    bench.py (stages recovered from the dispatch order of each forward)."""
+    import csv
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Dispatch_Id"]))
+    rows = [r for r in rows if "blt::" in r["Kernel_Name"]]
+    names = [r["Kernel_Name"] for r in rows]
+    # split into forwards: each starts with embed_kernel
+    starts = [i for i, n in enumerate(names) if "embed_kernel" in n] + [len(names)]
+    agg = {}
+    for a, b in zip(starts[:-1], starts[1:]):
+        for st, r in zip(_dispatch_stages(names[a:b], 14), rows[a:b]):
+            if st is None:
+                continue
+            kn = r["Kernel_Name"]
+            d = agg.setdefault(st, [0, 0.0, kn[:kn.rfind("(")]])
+            d[0] += 1
+            d[1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    print("| stage | kernel | launches | mean us | total us |")
+    print("|---|---|---|---|---|")
+    for st, (n, us, k) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        print("| %s | `%s` | %d | %.1f | %.0f |" % (st, k, n, us / n, us))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -56,7 +144,22 @@ def main():
     ap.add_argument("--cpu-seq", type=int, default=4096,
                     help="tokens of the CPU-oracle sample (B=1)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles",
+                                                           "traffic_config4.json"),
+                    help="per-stage HBM bytes per launch measured with rocprofv3 --pmc")
+    ap.add_argument("--summarize", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR",
+                                                     "COPY_WRITE_DIR"),
+                    help="print per-stage traffic from rocprofv3 --pmc output and exit")
+    ap.add_argument("--copy-bytes", type=float, default=float(2 ** 30))
+    ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
+                    help="print per-stage kernel durations from rocprofv3 --kernel-trace output")
     args = ap.parse_args()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace)
+        return
+    if args.summarize:
+        summarize(args)
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(rows shard with no collective; see DESIGN.md). Run with --gpus 1.",
@@ -120,9 +223,14 @@ def main():
     ms_tot, launches = mfma_stages[dom]
     per_launch_ms = ms_tot / launches
     achieved = stage_flops(dom, Mtok, B, T, D, F, V, H, W) / (per_launch_ms * 1e-3) / 1e12
+    traffic = None
+    if os.path.exists(args.traffic_file) and (B, T, W) == (16, 8192, 512):
+        st = json.load(open(args.traffic_file)).get("stages", {}).get(dom)
+        if st:
+            traffic = int(st["fetch_bytes"] + st["write_bytes"])
     roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                 "launch_ms": round(per_launch_ms, 4)}
     step_tflops = total_flops / sec / 1e12
     result = {

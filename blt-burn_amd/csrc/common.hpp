@@ -42,17 +42,26 @@ __host__ __device__ inline float bf16_to_f32(uint16_t h) {
   return f;
 }
 
-// Round to nearest even; NaN stays NaN.
+// Round to nearest even; NaN stays NaN.  On the device this is the gfx950
+// v_cvt_pk_bf16_f32 instruction; the host path is the same rounding in integers.
 __host__ __device__ inline uint16_t f32_to_bf16(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+#else
   uint32_t u;
   __builtin_memcpy(&u, &f, 4);
   if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
   u += 0x7fffu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);
+#endif
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// two floats -> packed bf16 pair (lo in bits 0..15), one v_cvt_pk_bf16_f32
 __device__ inline uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+  bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // ---- wave64 reductions -----------------------------------------------------

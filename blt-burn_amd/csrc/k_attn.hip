@@ -83,25 +83,25 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
     const uint16_t* qrow = p.q + b * p.sb_q + h * p.sh_q + (qi < T ? qi : 0) * p.st_q;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      uint4 t = qi < T ? *reinterpret_cast<const uint4*>(qrow + ks * 16 + lhalf * 8)
-                       : make_uint4(0, 0, 0, 0);
+      u32x4_t t = qi < T ? *reinterpret_cast<const u32x4_t*>(qrow + ks * 16 + lhalf * 8)
+                         : u32x4_t{0, 0, 0, 0};
       qf[ks] = __builtin_bit_cast(bf16x8_t, t);
     }
   }
 
   // K/V tile staging: thread -> (key, 16-byte chunk) for two chunks each of K and V
-  uint4 rk[2], rv[2];
+  u32x4_t rk[2], rv[2];
   auto gload = [&](int t) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int id2 = tid + 256 * i, key = id2 >> 3, c = id2 & 7;
       const int64_t kk = (int64_t)t * BKV + key;
       if (kk < T) {
-        rk[i] = *reinterpret_cast<const uint4*>(kbase + kk * p.st_k + c * 8);
-        rv[i] = *reinterpret_cast<const uint4*>(vbase + kk * p.st_v + c * 8);
+        rk[i] = *reinterpret_cast<const u32x4_t*>(kbase + kk * p.st_k + c * 8);
+        rv[i] = *reinterpret_cast<const u32x4_t*>(vbase + kk * p.st_v + c * 8);
       } else {
-        rk[i] = make_uint4(0, 0, 0, 0);
-        rv[i] = make_uint4(0, 0, 0, 0);
+        rk[i] = u32x4_t{0, 0, 0, 0};
+        rv[i] = u32x4_t{0, 0, 0, 0};
       }
     }
   };
@@ -111,7 +111,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int id2 = tid + 256 * i, key = id2 >> 3, c = id2 & 7;
-      *reinterpret_cast<uint4*>(sk + kswz(key, c)) = rk[i];
+      *reinterpret_cast<u32x4_t*>(sk + kswz(key, c)) = rk[i];
       const uint16_t* e = reinterpret_cast<const uint16_t*>(&rv[i]);
 #pragma unroll
       for (int j = 0; j < 8; ++j) sv[(c * 8 + j) * VT_LD + key] = e[j];
@@ -150,32 +150,43 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
           s[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], s[sub], 0, 0, 0);
         }
       }
-      // ---- scale, mask, online softmax ----
+      // ---- mask, online softmax (log2 domain, scale folded into one FMA) ----
+      // The running max used for exponentiation (m) only moves when a row's
+      // max grows by more than 2^8 (checked wave-wide), so P <= 256 and the
+      // O / l rescale is skipped for most tiles; O / l is unchanged by it.
       const bool need_mask = (p.causal && kb + BKV - 1 > qw) ||
                              (window > 0 && kb <= qw + 31 - window) || (kb + BKV > T);
-      float mt = -INFINITY;
+      if (need_mask) {
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
+        for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = s[sub][r] * sl2;
-          if (need_mask) {
+          for (int r = 0; r < 16; ++r) {
             const int64_t key = kb + sub * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
             bool vis = key < T;
             if (p.causal) {
               vis = vis && key <= qi;
               if (window > 0) vis = vis && key > qi - window;
             }
-            x = vis ? x : -INFINITY;
+            s[sub][r] = vis ? s[sub][r] : -INFINITY;
           }
-          s[sub][r] = x;
-          mt = fmaxf(mt, x);
-        }
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      const float m_new = fmaxf(m, mt);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m - m_use);
-      m = m_new;
+      }
+      float mt = -INFINITY;
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[sub][r]);
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * sl2;
+      if (__any(mt > m + 8.f)) {
+        const float m_new = fmaxf(m, mt);
+        const float alpha = m_new == -INFINITY ? 1.f : exp2f(m - m_new);
+        m = m_new;
+        l *= alpha;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
+      }
+      const float m_use = m == -INFINITY ? 0.f : m;
       float ls = 0.f;
       bf16x8_t pb[2][2];
 #pragma unroll
@@ -185,18 +196,14 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
           uint32_t w[4];
 #pragma unroll
           for (int e = 0; e < 8; e += 2) {
-            const float p0 = exp2f(s[sub][8 * u + e] - m_use);
-            const float p1 = exp2f(s[sub][8 * u + e + 1] - m_use);
+            const float p0 = exp2f(fmaf(s[sub][8 * u + e], sl2, -m_use));
+            const float p1 = exp2f(fmaf(s[sub][8 * u + e + 1], sl2, -m_use));
             ls += p0 + p1;
             w[e >> 1] = pack_bf16x2(p0, p1);
           }
-          pb[sub][u] = __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
+          pb[sub][u] = __builtin_bit_cast(bf16x8_t, u32x4_t{w[0], w[1], w[2], w[3]});
         }
-      l = l * alpha + ls;
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
+      l += ls;
       // ---- O^T += V^T . P^T ----
 #pragma unroll
       for (int dsub = 0; dsub < 2; ++dsub) {
@@ -206,10 +213,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             const int k0 = sub * 32 + u * 16 + 4 * lhalf;
-            const uint2 lo4 = *reinterpret_cast<const uint2*>(vrow + k0);
-            const uint2 hi4 = *reinterpret_cast<const uint2*>(vrow + k0 + 8);
-            const bf16x8_t a =
-                __builtin_bit_cast(bf16x8_t, make_uint4(lo4.x, lo4.y, hi4.x, hi4.y));
+            const u32x2_t lo4 = *reinterpret_cast<const u32x2_t*>(vrow + k0);
+            const u32x2_t hi4 = *reinterpret_cast<const u32x2_t*>(vrow + k0 + 8);
+            const bf16x8_t a = __builtin_bit_cast(bf16x8_t, u32x4_t{lo4.x, lo4.y, hi4.x, hi4.y});
             o[dsub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[sub][u], o[dsub], 0, 0, 0);
           }
       }
@@ -227,10 +233,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int d0 = dsub * 32 + 8 * j + 4 * lhalf;
-      uint2 w;
+      u32x2_t w;
       w.x = pack_bf16x2(o[dsub][4 * j] * inv, o[dsub][4 * j + 1] * inv);
       w.y = pack_bf16x2(o[dsub][4 * j + 2] * inv, o[dsub][4 * j + 3] * inv);
-      *reinterpret_cast<uint2*>(orow + d0) = w;
+      *reinterpret_cast<u32x2_t*>(orow + d0) = w;
     }
 }
 
