@@ -17,6 +17,7 @@ c_vp = ctypes.c_void_p
 BLT_OK = 0
 EPS_AFTER_SQRT, EPS_INSIDE_SQRT = 0, 1
 PATCH_MONOTONIC, PATCH_GLOBAL = 0, 1
+EPI_BF16, EPI_F32, EPI_RESID_F32, EPI_QKV_ROPE, EPI_SILU_GATE = 0, 1, 2, 3, 4
 NUM_STAGES = 11
 
 EXPORTS = {
@@ -52,6 +53,8 @@ EXPORTS = {
     "blt_synth_normal_bf16": (c_i32, [c_u64, c_vp, c_i64, c_f64, c_f64]),
     "blt_synth_tokens": (c_i32, [c_u64, c_vp, c_i64, c_f64, c_f64, c_i32]),
     "blt_gemm_bf16": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp]),
+    "blt_gemm_bf16_epilogue": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                       c_i32, c_i32, c_i32, c_i64, c_vp, c_vp]),
 }
 
 

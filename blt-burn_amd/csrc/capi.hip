@@ -379,4 +379,33 @@ int blt_gemm_bf16(const uint16_t* A, const uint16_t* Bt, uint16_t* C, int64_t M,
   return launch_gemm(g, STREAM(stream));
 }
 
+int blt_gemm_bf16_epilogue(const uint16_t* A, const uint16_t* Bt, void* C, int64_t M, int64_t N,
+                           int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int32_t epilogue,
+                           int32_t n_valid, int32_t rope_cols, int64_t seq_len,
+                           const float* rope_cs, blt_stream_t stream) {
+  if (epilogue < BLT_EPI_BF16 || epilogue > BLT_EPI_SILU_GATE)
+    return fail(BLT_ERR_INVALID, "gemm_epilogue: bad epilogue");
+  if (M < 0 || N <= 0 || K <= 0 || K % 64 != 0 || lda < K || ldb < K)
+    return fail(BLT_ERR_SHAPE, "gemm_epilogue: need K % 64 == 0, lda, ldb >= K");
+  if (epilogue != BLT_EPI_F32 && N % 64 != 0)
+    return fail(BLT_ERR_SHAPE, "gemm_epilogue: N % 64 == 0 for this epilogue");
+  const int64_t out_cols = epilogue == BLT_EPI_SILU_GATE ? N / 2
+                           : epilogue == BLT_EPI_F32    ? n_valid
+                                                        : N;
+  if (epilogue == BLT_EPI_F32 && (n_valid <= 0 || n_valid > N))
+    return fail(BLT_ERR_SHAPE, "gemm_epilogue: 0 < n_valid <= N");
+  if (ldc < out_cols) return fail(BLT_ERR_SHAPE, "gemm_epilogue: ldc too small");
+  if (epilogue == BLT_EPI_QKV_ROPE &&
+      (rope_cols < 0 || rope_cols % 64 != 0 || rope_cols > N || seq_len <= 0 ||
+       (rope_cols > 0 && rope_cs == nullptr)))
+    return fail(BLT_ERR_SHAPE, "gemm_epilogue: rope needs rope_cols % 64 == 0, seq_len > 0, table");
+  if (M == 0) return BLT_OK;
+  if (!A || !Bt || !C) return fail(BLT_ERR_INVALID, "gemm_epilogue: null pointer");
+  GemmArgs g{};
+  g.A = A; g.Bt = Bt; g.C = C; g.M = M; g.N = N; g.K = K;
+  g.lda = lda; g.ldb = ldb; g.ldc = ldc; g.epi = epilogue; g.n_valid = n_valid;
+  g.rope_cols = rope_cols; g.seq_len = seq_len; g.rope_cs = rope_cs;
+  return launch_gemm(g, STREAM(stream));
+}
+
 }  // extern "C"

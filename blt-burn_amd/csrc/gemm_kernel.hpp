@@ -57,119 +57,15 @@ struct GemmCfg {
   static_assert(BK == 32 || BK == 64, "BK is 32 or 64");
 };
 
-template <int BM, int BN, int BK, int WM, int WN, int PF, int OCC>
-__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(OCC)))
-void gemm_bf16_kernel(GemmArgs p) {
-  using C = GemmCfg<BM, BN, BK, WM, WN>;
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * C::STAGE];
-
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int wm = wid / WN, wn = wid % WN;
-
-  // XCD-aware tile order: dispatch round-robins blocks over 8 XCDs; give each
-  // XCD a contiguous run of tiles (N fastest) so A rows are reused from its L2.
-  const int ntm = (int)((p.M + BM - 1) / BM), ntn = (int)((p.N + BN - 1) / BN);
-  const int nb = ntm * ntn;
-  const int bid = blockIdx.x;
-  const int nb8 = nb & ~7;
-  const int id = bid < nb8 ? (bid & 7) * (nb8 >> 3) + (bid >> 3) : bid;
-  const int64_t m0 = (int64_t)(id / ntn) * BM;
-  const int64_t n0 = (int64_t)(id % ntn) * BN;
-
-  // Global source rows are clamped into range: rows past M (or N) load a
-  // valid row whose results land in rows/columns that are never stored.
-  const int64_t am = p.M - 1 - m0, bn = p.N - 1 - n0;
-
-  // PF register sets: K tile t is staged in set t % PF, so the loads of
-  // tiles kt+1 .. kt+PF are in flight while tile kt feeds the MFMAs.
-  u32x4_t ra[PF][C::A_LD], rb[PF][C::B_LD];
-  auto gload = [&](u32x4_t (&xa)[C::A_LD], u32x4_t (&xb)[C::B_LD], int kt) {
-    const int64_t k0 = (int64_t)kt * BK;
-#pragma unroll
-    for (int i = 0; i < C::A_LD; ++i) {
-      const int id2 = tid + C::NT * i, r = id2 / C::CH, c = id2 % C::CH;
-      const int64_t gr = m0 + (r < am ? r : am);
-      xa[i] = *reinterpret_cast<const u32x4_t*>(p.A + gr * p.lda + k0 + c * 8);
-    }
-#pragma unroll
-    for (int i = 0; i < C::B_LD; ++i) {
-      const int id2 = tid + C::NT * i, r = id2 / C::CH, c = id2 % C::CH;
-      const int64_t gr = n0 + (r < bn ? r : bn);
-      xb[i] = *reinterpret_cast<const u32x4_t*>(p.Bt + gr * p.ldb + k0 + c * 8);
-    }
-  };
-  auto sstore = [&](const u32x4_t (&xa)[C::A_LD], const u32x4_t (&xb)[C::B_LD], int stage) {
-    uint16_t* sa = lds + stage * C::STAGE;
-    uint16_t* sb = sa + BM * BK;
-#pragma unroll
-    for (int i = 0; i < C::A_LD; ++i) {
-      const int id2 = tid + C::NT * i, r = id2 / C::CH, c = id2 % C::CH;
-      *reinterpret_cast<u32x4_t*>(sa + swz<BK>(r, c)) = xa[i];
-    }
-#pragma unroll
-    for (int i = 0; i < C::B_LD; ++i) {
-      const int id2 = tid + C::NT * i, r = id2 / C::CH, c = id2 % C::CH;
-      *reinterpret_cast<u32x4_t*>(sb + swz<BK>(r, c)) = xb[i];
-    }
-  };
-
-  f32x16_t acc[C::TM][C::TN];
-#pragma unroll
-  for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  const int lrow = lane & 31, lhalf = lane >> 5;
-  auto compute = [&](int stage) {
-    const uint16_t* sa = lds + stage * C::STAGE;
-    const uint16_t* sb = sa + BM * BK;
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int chunk = ks * 2 + lhalf;
-      bf16x8_t af[C::TM], bfr[C::TN];
-#pragma unroll
-      for (int i = 0; i < C::TM; ++i)
-        af[i] = *reinterpret_cast<const bf16x8_t*>(sa + swz<BK>(wm * C::WTM + i * 32 + lrow, chunk));
-#pragma unroll
-      for (int j = 0; j < C::TN; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8_t*>(sb + swz<BK>(wn * C::WTN + j * 32 + lrow, chunk));
-#pragma unroll
-      for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
-    }
-  };
-
-  const int KT = (int)(p.K / BK);
-  // prologue: tile 0 -> LDS stage 0, tiles 1 .. PF in flight in their sets
-  gload(ra[0], rb[0], 0);
-  sstore(ra[0], rb[0], 0);
-#pragma unroll
-  for (int t = 1; t <= PF; ++t)
-    if (t < KT) gload(ra[t % PF], rb[t % PF], t);
-  __syncthreads();
-
-  for (int kt0 = 0; kt0 < KT; kt0 += PF) {
-    static_for<0, PF>([&](auto uc) {
-      constexpr int nx = (decltype(uc)::value + 1) % PF;  // set holding tile kt + 1
-      const int kt = kt0 + decltype(uc)::value;
-      if (kt < KT) {
-        compute(kt & 1);
-        if (kt + 1 < KT) sstore(ra[nx], rb[nx], (kt + 1) & 1);
-        if (kt + 1 + PF < KT) gload(ra[nx], rb[nx], kt + 1 + PF);
-        __syncthreads();
-      }
-    });
-  }
-
-  // ---- epilogue.  The MFMAs computed the transposed tile (B operand = A rows),
-  // so acc[i][j][r] is C[row][col] with row = m-tile i + lane % 32 and
-  // col = n-tile j + 8 * (r / 4) + 4 * (lane / 32) + r % 4: each lane owns one
-  // output row and 4 consecutive columns per register group, which the
-  // epilogues store as one 8-byte (bf16) or 16-byte (f32) vector.
+// ---- epilogue, shared by the kernels below.  The MFMAs computed the
+// transposed tile (B operand = A rows), so acc[i][j][r] is C[row][col] with
+// row = m-tile i + lane % 32 and col = n-tile j + 8 * (r / 4) + 4 * (lane / 32)
+// + r % 4: each lane owns one output row and 4 consecutive columns per
+// register group, which the epilogues store as one 8-byte (bf16) or 16-byte
+// (f32) vector.
+template <class C>
+__device__ inline void epilogue(const GemmArgs& p, f32x16_t (&acc)[C::TM][C::TN], int64_t m0,
+                                int64_t n0, int wm, int wn, int lrow, int lhalf) {
   const int64_t row_base = m0 + wm * C::WTM + lrow;
   const int64_t col_base = n0 + wn * C::WTN + 4 * lhalf;
   if (p.epi == EPI_QKV_ROPE || p.epi == EPI_SILU_GATE) {
@@ -270,6 +166,422 @@ void gemm_bf16_kernel(GemmArgs p) {
         }
       }
   }
+}
+
+// Tile order.  Dispatch round-robins blocks over the 8 XCDs; each XCD gets a
+// contiguous run of tile ids, and ids walk groups of group_m M-tiles with M
+// fastest inside a group, so the blocks resident on one XCD share group_m A
+// row-tiles and a few Bt column-tiles in that XCD's L2 (group_m = 0: N fastest).
+template <int BM, int BN>
+__device__ inline void tile_origin(const GemmArgs& p, int64_t& m0, int64_t& n0) {
+  const int ntm = (int)((p.M + BM - 1) / BM), ntn = (int)((p.N + BN - 1) / BN);
+  const int nb = ntm * ntn;
+  const int bid = blockIdx.x;
+  const int nb8 = nb & ~7;
+  const int id = bid < nb8 ? (bid & 7) * (nb8 >> 3) + (bid >> 3) : bid;
+  int tm, tn;
+  if (p.group_m > 0) {
+    const int gsz = p.group_m * ntn;
+    const int g = id / gsz, first = g * p.group_m;
+    const int gm = ntm - first < p.group_m ? ntm - first : p.group_m;
+    const int local = id - g * gsz;
+    tm = first + local % gm;
+    tn = local / gm;
+  } else {
+    tm = id / ntn;
+    tn = id % ntn;
+  }
+  m0 = (int64_t)tm * BM;
+  n0 = (int64_t)tn * BN;
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int PF, int OCC>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(OCC)))
+void gemm_bf16_kernel(GemmArgs p) {
+  using C = GemmCfg<BM, BN, BK, WM, WN>;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * C::STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wm = wid / WN, wn = wid % WN;
+
+  int64_t m0, n0;
+  tile_origin<BM, BN>(p, m0, n0);
+
+  // Global source rows are clamped into range: rows past M (or N) load a
+  // valid row whose results land in rows/columns that are never stored.
+  const int64_t am = p.M - 1 - m0, bn = p.N - 1 - n0;
+
+  // PF register sets: K tile t is staged in set t % PF, so the loads of
+  // tiles kt+1 .. kt+PF are in flight while tile kt feeds the MFMAs.
+  u32x4_t ra[PF][C::A_LD], rb[PF][C::B_LD];
+  auto gload = [&](u32x4_t (&xa)[C::A_LD], u32x4_t (&xb)[C::B_LD], int kt) {
+    const int64_t k0 = (int64_t)kt * BK;
+#pragma unroll
+    for (int i = 0; i < C::A_LD; ++i) {
+      const int id2 = tid + C::NT * i, r = id2 / C::CH, c = id2 % C::CH;
+      const int64_t gr = m0 + (r < am ? r : am);
+      xa[i] = *reinterpret_cast<const u32x4_t*>(p.A + gr * p.lda + k0 + c * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < C::B_LD; ++i) {
+      const int id2 = tid + C::NT * i, r = id2 / C::CH, c = id2 % C::CH;
+      const int64_t gr = n0 + (r < bn ? r : bn);
+      xb[i] = *reinterpret_cast<const u32x4_t*>(p.Bt + gr * p.ldb + k0 + c * 8);
+    }
+  };
+  auto sstore = [&](const u32x4_t (&xa)[C::A_LD], const u32x4_t (&xb)[C::B_LD], int stage) {
+    uint16_t* sa = lds + stage * C::STAGE;
+    uint16_t* sb = sa + BM * BK;
+#pragma unroll
+    for (int i = 0; i < C::A_LD; ++i) {
+      const int id2 = tid + C::NT * i, r = id2 / C::CH, c = id2 % C::CH;
+      *reinterpret_cast<u32x4_t*>(sa + swz<BK>(r, c)) = xa[i];
+    }
+#pragma unroll
+    for (int i = 0; i < C::B_LD; ++i) {
+      const int id2 = tid + C::NT * i, r = id2 / C::CH, c = id2 % C::CH;
+      *reinterpret_cast<u32x4_t*>(sb + swz<BK>(r, c)) = xb[i];
+    }
+  };
+
+  f32x16_t acc[C::TM][C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  auto compute = [&](int stage) {
+    const uint16_t* sa = lds + stage * C::STAGE;
+    const uint16_t* sb = sa + BM * BK;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const int chunk = ks * 2 + lhalf;
+      bf16x8_t af[C::TM], bfr[C::TN];
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+        af[i] = *reinterpret_cast<const bf16x8_t*>(sa + swz<BK>(wm * C::WTM + i * 32 + lrow, chunk));
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+        bfr[j] = *reinterpret_cast<const bf16x8_t*>(sb + swz<BK>(wn * C::WTN + j * 32 + lrow, chunk));
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  const int KT = (int)(p.K / BK);
+  // prologue: tile 0 -> LDS stage 0, tiles 1 .. PF in flight in their sets
+  gload(ra[0], rb[0], 0);
+  sstore(ra[0], rb[0], 0);
+#pragma unroll
+  for (int t = 1; t <= PF; ++t)
+    if (t < KT) gload(ra[t % PF], rb[t % PF], t);
+  __syncthreads();
+
+  for (int kt0 = 0; kt0 < KT; kt0 += PF) {
+    static_for<0, PF>([&](auto uc) {
+      constexpr int nx = (decltype(uc)::value + 1) % PF;  // set holding tile kt + 1
+      const int kt = kt0 + decltype(uc)::value;
+      if (kt < KT) {
+        compute(kt & 1);
+        if (kt + 1 < KT) sstore(ra[nx], rb[nx], (kt + 1) & 1);
+        if (kt + 1 + PF < KT) gload(ra[nx], rb[nx], kt + 1 + PF);
+        __syncthreads();
+      }
+    });
+  }
+
+  epilogue<C>(p, acc, m0, n0, wm, wn, lrow, lhalf);
+}
+
+// ---- LDS-staged epilogue for the DMA kernel.  After the main loop each wave
+// owns its (WTM x WTN) accumulator tile; it writes the finished values of 32
+// (f32 outputs) or 64 (bf16 outputs) rows at a time into a private LDS region
+// in row-major order, then streams them out as whole 16-byte pieces of rows,
+// so a store instruction covers a few full cache lines instead of 32 rows.
+// `smem` is the block's LDS (free after the main loop); each wave uses
+// its own slice of `region` bytes.
+// Lanes of one wave exchange data through LDS below.  A wave's LDS operations
+// execute in order, but the compiler only sees per-lane addresses: this
+// fence stops it from moving LDS accesses across the phase boundary and
+// waits for the wave's outstanding LDS operations.
+__device__ inline void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+template <class C>
+__device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C::TN], int64_t m0,
+                                    int64_t n0, int wid, int wm, int wn, int lane,
+                                    unsigned char* smem) {
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  const int64_t row0 = m0 + wm * C::WTM;  // first row of this wave's tile
+  const int64_t col0 = n0 + wn * C::WTN;  // first column (pre-epilogue index)
+  if (p.epi == EPI_RESID_F32 || p.epi == EPI_F32) {
+    constexpr int LD = C::WTN + 2;  // f32 row pitch (8-byte pad)
+    float* buf = reinterpret_cast<float*>(smem) + wid * 32 * LD;
+    constexpr int CPR = C::WTN / 4;  // 16-byte pieces per row
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float* d = buf + lrow * LD + j * 32 + 8 * g + 4 * lhalf;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) d[e] = acc[i][j][4 * g + e];
+        }
+      wave_lds_fence();
+#pragma unroll
+      for (int t = 0; t < 32 * CPR / 64; ++t) {
+        const int q = lane + 64 * t, r = q / CPR, c = q % CPR;
+        const int64_t row = row0 + i * 32 + r;
+        const int64_t col = col0 + c * 4;
+        const float* sp = buf + r * LD + c * 4;
+        f32x4_t v = f32x4_t{sp[0], sp[1], sp[2], sp[3]};
+        if (row >= p.M || col >= p.N) continue;
+        float* o = reinterpret_cast<float*>(p.C) + row * p.ldc + col;
+        if (p.epi == EPI_RESID_F32) {
+          const f32x4_t x = *reinterpret_cast<const f32x4_t*>(o);
+          v += x;
+          *reinterpret_cast<f32x4_t*>(o) = v;
+        } else if (col + 3 < p.n_valid && p.vec_ok) {
+          *reinterpret_cast<f32x4_t*>(o) = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (col + e < p.n_valid) o[e] = v[e];
+        }
+      }
+      wave_lds_fence();
+    }
+    return;
+  }
+  // bf16 outputs: BF16 (WTN columns), QKV_ROPE (WTN), SILU_GATE (WTN / 2)
+  const bool silu = p.epi == EPI_SILU_GATE;
+  constexpr int LD = C::WTN + 4;  // bf16 row pitch (8-byte pad)
+  uint16_t* buf = reinterpret_cast<uint16_t*>(smem) + wid * 64 * LD;
+#pragma unroll
+  for (int i0 = 0; i0 < C::TM; i0 += 2) {
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const int i = i0 + ii;
+      const int rl = ii * 32 + lrow;  // row within this 64-row slab
+      const int64_t row = row0 + i * 32 + lrow;
+      const int64_t pos = p.epi == EPI_QKV_ROPE ? row % p.seq_len : 0;
+      if (p.epi == EPI_BF16) {
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<u32x2_t*>(buf + rl * LD + j * 32 + 8 * g + 4 * lhalf) =
+                u32x2_t{pack_bf16x2(acc[i][j][4 * g], acc[i][j][4 * g + 1]),
+                        pack_bf16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3])};
+        continue;
+      }
+#pragma unroll
+      for (int j = 0; j < C::TN; j += 2)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int cl = j * 32 + 8 * g + 4 * lhalf;  // column within the wave tile
+          float x1[4], x2[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            x1[e] = acc[i][j][4 * g + e];
+            x2[e] = acc[i][j + 1][4 * g + e];
+          }
+          if (silu) {
+            float o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = (x1[e] / (1.f + __expf(-x1[e]))) * x2[e];
+            *reinterpret_cast<u32x2_t*>(buf + rl * LD + (j / 2) * 32 + 8 * g + 4 * lhalf) =
+                u32x2_t{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+          } else {
+            float o1[4], o2[4];
+            if (col0 + cl < p.rope_cols) {
+              const float* cs = p.rope_cs + (pos * 32 + (cl & 31)) * 2;
+              const f32x4_t c01 = *reinterpret_cast<const f32x4_t*>(cs);
+              const f32x4_t c23 = *reinterpret_cast<const f32x4_t*>(cs + 4);
+              const float cv[4] = {c01.x, c01.z, c23.x, c23.z};
+              const float sv[4] = {c01.y, c01.w, c23.y, c23.w};
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                o1[e] = x1[e] * cv[e] - x2[e] * sv[e];
+                o2[e] = x1[e] * sv[e] + x2[e] * cv[e];
+              }
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                o1[e] = x1[e];
+                o2[e] = x2[e];
+              }
+            }
+            *reinterpret_cast<u32x2_t*>(buf + rl * LD + cl) =
+                u32x2_t{pack_bf16x2(o1[0], o1[1]), pack_bf16x2(o1[2], o1[3])};
+            *reinterpret_cast<u32x2_t*>(buf + rl * LD + cl + 32) =
+                u32x2_t{pack_bf16x2(o2[0], o2[1]), pack_bf16x2(o2[2], o2[3])};
+          }
+        }
+    }
+    wave_lds_fence();
+    // stream the 64-row slab out: OW columns per row in 16-byte pieces
+    const int OW = silu ? C::WTN / 2 : C::WTN;
+    const int CPR = OW / 8;
+    const int64_t ocol0 = silu ? col0 / 2 : col0;
+    for (int q = lane; q < 64 * CPR; q += 64) {
+      const int r = q / CPR, c = q % CPR;
+      const int64_t row = row0 + i0 * 32 + r;
+      const uint16_t* sp = buf + r * LD + c * 8;
+      const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(sp);
+      const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(sp + 4);
+      if (row < p.M)
+        *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(p.C) + row * p.ldc + ocol0 +
+                                    c * 8) = u32x4_t{lo.x, lo.y, hi.x, hi.y};
+    }
+    wave_lds_fence();
+  }
+}
+
+// 16 bytes per lane from global memory straight into LDS (gfx950
+// global_load_lds_dwordx4): lane i's data lands at LDS byte lds_addr + 16 * i.
+// Issued from inline asm so the compiler does not serialise it against later
+// LDS reads; the caller orders it with dma_wait_barrier.  M0 is restored.
+__device__ inline void dma16(const void* g, unsigned lds_addr) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_addr), "v"(g)
+      : "memory");
+}
+
+// Wait until at most N of this wave's vector-memory loads are outstanding and
+// its LDS operations are done, then barrier; the memory clobber keeps the
+// compiler from moving LDS accesses across it.
+template <int N>
+__device__ inline void dma_wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Same tiling and epilogues as gemm_bf16_kernel, but K tiles are moved
+// global -> LDS by the LDS-DMA path (no VGPR staging, no ds_write) into S LDS
+// stages, with S - 1 tiles in flight: tile kt + S - 1 is issued into the stage
+// that tile kt - 1 freed before tile kt is consumed.  Each wave issues NI
+// 1-KB DMA chunks per K tile; a chunk is RPC LDS rows of BK bf16, and lane i
+// fetches the global 16-byte piece that the swizzle places at row i / CH,
+// slot i % CH.
+template <int BM, int BN, int BK, int WM, int WN, int S, int OCC>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(OCC)))
+void gemm_bf16_dma_kernel(GemmArgs p) {
+  using C = GemmCfg<BM, BN, BK, WM, WN>;
+  constexpr int NW = WM * WN;
+  constexpr int RPC = 64 / C::CH;        // LDS rows per 1-KB chunk
+  constexpr int RPB = 128 / BK;          // rows per 256 bytes (swizzle period)
+  constexpr int NCH = (BM + BN) / RPC;   // 1-KB chunks per stage
+  constexpr int NI = NCH / NW;         // chunks per wave per stage
+  static_assert(NCH % NW == 0, "DMA chunks must divide over the waves");
+  static_assert(S >= 2, "at least two LDS stages");
+  static_assert(NW * 64 * (C::WTN + 4) * 2 <= S * C::STAGE * 2 &&
+                    NW * 32 * (C::WTN + 2) * 4 <= S * C::STAGE * 2,
+                "staged epilogue must fit in the K-loop LDS");
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[S * C::STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int wm = wid / WN, wn = wid % WN;
+  int64_t m0, n0;
+  tile_origin<BM, BN>(p, m0, n0);
+  const int64_t am = p.M - 1 - m0, bn = p.N - 1 - n0;
+  const unsigned lds_base = (unsigned)(uintptr_t)lds;
+
+  // This wave's NI chunks: per-lane source row pointers (fixed over K) and
+  // wave-uniform LDS offsets within a stage.
+  const uint16_t* gsrc[NI];
+  unsigned lofs[NI];
+#pragma unroll
+  for (int q = 0; q < NI; ++q) {
+    const int ci = wid * NI + q;
+    const bool isA = ci < BM / RPC;  // uniform
+    const int rb = (isA ? ci : ci - BM / RPC) * RPC;
+    const int r = rb + lane / C::CH;
+    const int c = (lane % C::CH) ^ ((r / RPB) & (C::CH - 1));
+    const uint16_t* base = isA ? p.A : p.Bt;
+    const int64_t ld = isA ? p.lda : p.ldb;
+    const int64_t row = isA ? m0 + (r < am ? r : am) : n0 + (r < bn ? r : bn);
+    gsrc[q] = base + row * ld + c * 8;
+    lofs[q] = (isA ? 0u : (unsigned)(BM * BK * 2)) + (unsigned)(rb * BK * 2);
+  }
+  auto dma_tile = [&](int kt, int stage) {
+    const int64_t k0 = (int64_t)kt * BK;
+    const unsigned sbase = lds_base + (unsigned)(stage * C::STAGE * 2);
+#pragma unroll
+    for (int q = 0; q < NI; ++q)
+      dma16(gsrc[q] + k0, __builtin_amdgcn_readfirstlane(sbase + lofs[q]));
+  };
+
+  f32x16_t acc[C::TM][C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  auto compute = [&](int stage) {
+    const uint16_t* sa = lds + stage * C::STAGE;
+    const uint16_t* sb = sa + BM * BK;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const int chunk = ks * 2 + lhalf;
+      bf16x8_t af[C::TM], bfr[C::TN];
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+        af[i] = *reinterpret_cast<const bf16x8_t*>(sa + swz<BK>(wm * C::WTM + i * 32 + lrow, chunk));
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+        bfr[j] = *reinterpret_cast<const bf16x8_t*>(sb + swz<BK>(wn * C::WTN + j * 32 + lrow, chunk));
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // Wait until tile kt's chunks have landed, allowing the `after` tiles issued
+  // later (0 .. S-2 of them) to stay in flight, then barrier.
+  auto wait_tile = [&](int after) {
+    static_for<0, S - 1>([&](auto ic) {
+      if (after == decltype(ic)::value) dma_wait_barrier<NI * decltype(ic)::value>();
+    });
+  };
+  const int KT = (int)(p.K / BK);
+  const int pre = KT < S - 1 ? KT : S - 1;  // tiles issued in the prologue
+  for (int t = 0; t < pre; ++t) dma_tile(t, t);
+  wait_tile(pre - 1);
+  int st = 0;  // stage of tile kt
+  for (int kt = 0; kt < KT; ++kt) {
+    if (kt + S - 1 < KT) {
+      const int ns = st == 0 ? S - 1 : st - 1;  // stage (kt + S - 1) % S
+      dma_tile(kt + S - 1, ns);
+    }
+    compute(st);
+    if (kt + 1 < KT) {
+      const int last = kt + S - 1 < KT - 1 ? kt + S - 1 : KT - 1;  // newest tile issued
+      wait_tile(last - (kt + 1));
+    }
+    st = st + 1 < S ? st + 1 : 0;
+  }
+
+  // every wave is past its last LDS read of the K loop before LDS is reused
+  __syncthreads();
+  epilogue_lds<C>(p, acc, m0, n0, wid, wm, wn, lane, reinterpret_cast<unsigned char*>(lds));
 }
 
 }  // namespace gemm

@@ -4,6 +4,15 @@
 namespace blt {
 
 namespace {
+template <int BM, int BN, int BK, int WM, int WN, int S, int OCC>
+int run_gemm_dma(const GemmArgs& a, hipStream_t s) {
+  const int64_t nb = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm::gemm_bf16_dma_kernel<BM, BN, BK, WM, WN, S, OCC>), dim3((unsigned)nb),
+                     dim3(64 * WM * WN), 0, s, a);
+  BLT_LAUNCH_CHECK("gemm_bf16_dma_kernel");
+  return 0;
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int PF, int OCC>
 int run_gemm(const GemmArgs& a, hipStream_t s) {
   const int64_t nb = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
@@ -23,9 +32,15 @@ int launch_gemm(const GemmArgs& a_in, hipStream_t s) {
        a.epi == EPI_SILU_GATE) && (a.N % 64 != 0 || a.ldc % 4 != 0 || (uintptr_t)a.C % 16 != 0))
     return fail(-2, "gemm: vector epilogues need N % 64 == 0, ldc % 4 == 0, 16-byte aligned C");
   if (a.K % 64 != 0) return fail(-2, "gemm: K must be a multiple of 64");
-  // N % 256 == 0: 128x256 tiles over 8 waves (wave tile 64x64, BK 32, two
-  // tiles in flight, 2 blocks per CU).  Otherwise 128x128 tiles over 4 waves.
-  if (a.N % 256 == 0) return run_gemm<128, 256, 32, 2, 4, 2, 2>(a, s);
+  if ((uintptr_t)a.A % 16 != 0 || (uintptr_t)a.Bt % 16 != 0 || a.lda % 8 != 0 || a.ldb % 8 != 0)
+    return fail(-2, "gemm: A and Bt rows must be 16-byte aligned (lda, ldb % 8 == 0)");
+  // Wide N (QKV, W1|W3): walk groups of 8 M-tiles so the blocks resident on
+  // an XCD share A and Bt tiles in its L2; narrow N (O, W2: 3 tiles): N fastest.
+  a.group_m = (a.N + 255) / 256 >= 8 ? 8 : 0;
+  // N % 256 == 0: 256x256 tiles over 8 waves (wave tile 128x64), K tiles of
+  // 64 moved by LDS DMA through 2 stages, LDS-staged epilogue.  Otherwise (the
+  // 260-wide head) 128x128 register-staged tiles over 4 waves.
+  if (a.N % 256 == 0) return run_gemm_dma<256, 256, 64, 2, 4, 2, 2>(a, s);
   return run_gemm<128, 128, 32, 2, 2, 2, 3>(a, s);
 }
 

@@ -47,6 +47,7 @@ struct GemmArgs {
   int64_t seq_len;  // EPI_QKV_ROPE: position = row % seq_len
   const float* rope_cs;  // [max_seqlen, 32, 2]
   int vec_ok;            // EPI_F32: C and ldc allow 16-byte row stores
+  int group_m;           // tile order: M-tiles per group (0 = N fastest)
 };
 int launch_gemm(const GemmArgs& a, hipStream_t s);
 

@@ -244,6 +244,30 @@ int blt_synth_tokens(uint64_t seed, int32_t* out, int64_t n, double zipf_s, doub
 int blt_gemm_bf16(const uint16_t* A, const uint16_t* Bt, uint16_t* C, int64_t M, int64_t N,
                   int64_t K, blt_stream_t stream);
 
+/* The same GEMM with each fused epilogue the model uses (for testing and
+ * benchmarking the kernels in isolation).  C = A[M,K] . Bt[N,K]^T, then:
+ *   BLT_EPI_BF16:      C bf16 [M, ldc]
+ *   BLT_EPI_F32:       C f32  [M, ldc], columns >= n_valid not written
+ *   BLT_EPI_RESID_F32: C f32  [M, ldc] += result
+ *   BLT_EPI_SILU_GATE: Bt rows in 64-row groups (32 gate rows, then the 32
+ *                      matching up rows); C bf16 [M, ldc] gets silu(gate) * up,
+ *                      N / 2 columns
+ *   BLT_EPI_QKV_ROPE:  C bf16 [M, ldc]; columns < rope_cols are rotated in
+ *                      64-wide heads (pairs (c, c + 32)) with the table rope_cs
+ *                      [>= seq_len, 32, 2] at position row % seq_len
+ * K % 64 == 0; N % 64 == 0 except for BLT_EPI_F32; rows 16-byte aligned. */
+typedef enum blt_epilogue {
+  BLT_EPI_BF16 = 0,
+  BLT_EPI_F32 = 1,
+  BLT_EPI_RESID_F32 = 2,
+  BLT_EPI_QKV_ROPE = 3,
+  BLT_EPI_SILU_GATE = 4
+} blt_epilogue;
+int blt_gemm_bf16_epilogue(const uint16_t* A, const uint16_t* Bt, void* C, int64_t M, int64_t N,
+                           int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int32_t epilogue,
+                           int32_t n_valid, int32_t rope_cols, int64_t seq_len,
+                           const float* rope_cs, blt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

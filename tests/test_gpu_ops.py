@@ -224,3 +224,71 @@ def test_attention_config3_b1():
     # config 3 shape at B=1 (the CPU comparison size): T=4096, 12 heads, window 512, RoPE
     o, ref = _attn_case(1, 12, 4096, True, 512, 10000.0, seed=synth.config_seed(3))
     np.testing.assert_allclose(o, ref, atol=2e-2, rtol=0)
+
+
+# ---------------------------------------------------------------- GEMM epilogues
+def _gemm_epi(a, bt, c, epi, n_valid=0, rope_cols=0, seq_len=1, cs=None):
+    M, K = a.shape
+    N = bt.shape[0]
+    _lib.check(_lib.lib().blt_gemm_bf16_epilogue(
+        a.data_ptr(), bt.data_ptr(), c.data_ptr(), M, N, K, K, K, c.shape[1], epi, n_valid,
+        rope_cols, seq_len, cs.data_ptr() if cs is not None else 0,
+        torch.cuda.current_stream().cuda_stream), "gemm_epilogue")
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 768, 768), (1000, 768, 2048), (4096, 768, 768)])
+def test_gemm_residual_epilogue(M, N, K):
+    a = torch.randn(M, K, device=DEV).to(torch.bfloat16)
+    bt = torch.randn(N, K, device=DEV).to(torch.bfloat16)
+    r0 = torch.randn(M, N, device=DEV)
+    c = r0.clone()
+    _gemm_epi(a, bt, c, _lib.EPI_RESID_F32)
+    ref = r0 + a.float() @ bt.float().t()
+    assert (c - ref).abs().max().item() <= 2e-3 * ref.abs().max().item()
+
+
+@pytest.mark.parametrize("M,N", [(256, 1024), (777, 4096)])
+def test_gemm_silu_gate_epilogue(M, N):
+    K = 768
+    a = torch.randn(M, K, device=DEV).to(torch.bfloat16)
+    bt = (0.1 * torch.randn(N, K, device=DEV)).to(torch.bfloat16)
+    c = torch.empty(M, N // 2, device=DEV, dtype=torch.bfloat16)
+    _gemm_epi(a, bt, c, _lib.EPI_SILU_GATE)
+    y = a.float() @ bt.float().t()
+    g = y.view(M, N // 64, 2, 32)[:, :, 0, :].reshape(M, N // 2)
+    u = y.view(M, N // 64, 2, 32)[:, :, 1, :].reshape(M, N // 2)
+    ref = torch.nn.functional.silu(g) * u
+    assert (c.float() - ref).abs().max().item() <= 2 ** -7 * ref.abs().max().item() + 1e-3
+
+
+@pytest.mark.parametrize("M,T", [(256, 256), (1000, 100), (8192, 4096)])
+def test_gemm_qkv_rope_epilogue(M, T):
+    K, N, rope_cols = 768, 2304, 1536
+    a = torch.randn(M, K, device=DEV).to(torch.bfloat16)
+    bt = (0.05 * torch.randn(N, K, device=DEV)).to(torch.bfloat16)
+    cs = torch.from_numpy(oracle.rope_table(64, T, 10000.0)).to(DEV)
+    c = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+    _gemm_epi(a, bt, c, _lib.EPI_QKV_ROPE, rope_cols=rope_cols, seq_len=T, cs=cs)
+    y = (a.float() @ bt.float().t()).cpu().numpy()
+    ref = y.copy()
+    pos = np.arange(M) % T
+    q = y[:, :rope_cols].reshape(M, rope_cols // 64, 64)
+    cos = cs.cpu().numpy()[pos, :, 0][:, None, :]
+    sin = cs.cpu().numpy()[pos, :, 1][:, None, :]
+    x1, x2 = q[..., :32], q[..., 32:]
+    ref[:, :rope_cols] = np.concatenate([x1 * cos - x2 * sin, x1 * sin + x2 * cos],
+                                        -1).reshape(M, rope_cols)
+    err = np.abs(c.float().cpu().numpy() - ref).max()
+    assert err <= 2 ** -7 * np.abs(ref).max() + 1e-3, err
+
+
+@pytest.mark.parametrize("M,N", [(300, 260), (4096, 260)])
+def test_gemm_f32_epilogue_partial_columns(M, N):
+    K = 768
+    a = torch.randn(M, K, device=DEV).to(torch.bfloat16)
+    bt = torch.randn(N, K, device=DEV).to(torch.bfloat16)
+    c = torch.full((M, N), 7.0, device=DEV)
+    _gemm_epi(a, bt, c, _lib.EPI_F32, n_valid=N)
+    ref = a.float() @ bt.float().t()
+    assert (c - ref).abs().max().item() <= 2e-3 * ref.abs().max().item()
