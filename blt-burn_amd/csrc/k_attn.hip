@@ -10,8 +10,9 @@
 // (lane ^ 32) instead of a 32-lane reduction.  The output is accumulated
 // transposed, O^T = V^T . P^T, which keeps the per-query rescale factor in
 // the lane that owns the query.  The P^T registers feed the MFMA B operand
-// directly (no LDS round trip); V is stored transposed in LDS with a
-// 136-byte row pitch so the 8-byte operand reads are bank-conflict free.
+// directly (no LDS round trip).  V stays row-major in LDS; the V^T operand is
+// read with ds_read_b64_tr_b16, whose 16-lane transpose hands each lane 4
+// consecutive keys of one head-dim column.
 //
 // Masking follows the reference's additive causal mask (model.rs:153-165:
 // key j visible to query i iff j <= i), extended with a window W > 0
@@ -26,10 +27,13 @@ namespace {
 constexpr int BQ = 128;     // queries per block
 constexpr int BKV = 64;     // keys per tile
 constexpr int D = 64;       // head dim
-constexpr int VT_LD = 68;   // V^T row pitch in bf16 (136 B)
+constexpr int V_LD = 72;    // V row pitch in bf16 (144 B): conflict-free transposing reads
 constexpr int K_TILE = BKV * D;
-constexpr int V_TILE = D * VT_LD;
+constexpr int V_TILE = BKV * V_LD;
 constexpr int STAGE = K_TILE + V_TILE;
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+#define LDS_PTR(p) ((__attribute__((address_space(3))) s16x4_t*)(p))
 
 // K rows are 128 B: chunk c of key row k is stored at c ^ ((k >> 1) & 7), so the
 // 16 rows one LDS cycle serves for an operand load fall in 16 distinct banks.
@@ -43,7 +47,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
 
   // XCD-aware order: consecutive query blocks of one (b, h) share K/V, so
   // keep them on one XCD (dispatch places block i on XCD i % 8).
-  const int nqb = (int)((p.T + BQ - 1) / BQ);
+  const int T = (int)p.T;
+  const int nqb = (T + BQ - 1) / BQ;
   const int64_t nb = (int64_t)nqb * p.H * p.B;
   const int64_t bid = blockIdx.x;
   const int64_t nb8 = nb & ~(int64_t)7;
@@ -52,57 +57,52 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
   const int64_t bh = id / nqb;
   const int64_t h = bh % p.H, b = bh / p.H;
 
-  const int64_t T = p.T;
-  const int64_t q0 = (int64_t)qb * BQ;
-  const int64_t qw = q0 + wid * 32;  // this wave's first query
+  const int q0 = qb * BQ;
+  const int qw = q0 + wid * 32;  // this wave's first query
   const int window = p.causal ? p.window : 0;
 
   // block key range
-  int64_t lo = 0, hi = T - 1;
+  int lo = 0, hi = T - 1;
   if (p.causal) {
     hi = q0 + BQ - 1 < T - 1 ? q0 + BQ - 1 : T - 1;
     if (window > 0) lo = q0 - window + 1 > 0 ? q0 - window + 1 : 0;
   }
-  const int t_begin = (int)(lo / BKV), t_end = (int)(hi / BKV);
+  const int t_begin = lo / BKV, t_end = hi / BKV;
   // wave key range
-  int64_t wlo = 0, whi = T - 1;
+  int wlo = 0, whi = T - 1;
   if (p.causal) {
     whi = qw + 31 < T - 1 ? qw + 31 : T - 1;
     if (window > 0) wlo = qw - window + 1 > 0 ? qw - window + 1 : 0;
   }
   const bool wave_active = qw < T;
-  const int wt_begin = (int)(wlo / BKV), wt_end = (int)(whi / BKV);
+  const int wt_begin = wlo / BKV, wt_end = whi / BKV;
 
   const uint16_t* kbase = p.k + b * p.sb_k + h * p.sh_k;
   const uint16_t* vbase = p.v + b * p.sb_v + h * p.sh_v;
 
   // Q fragments (B operand of S^T = K . Q^T): query qw + lrow, d = 16*ks + 8*lhalf .. +8
-  const int64_t qi = qw + lrow;
+  const int qi = qw + lrow;
   bf16x8_t qf[4];
   {
-    const uint16_t* qrow = p.q + b * p.sb_q + h * p.sh_q + (qi < T ? qi : 0) * p.st_q;
+    const int qc = qi < T ? qi : T - 1;  // rows past T load a valid row, never stored
+    const uint16_t* qrow = p.q + b * p.sb_q + h * p.sh_q + (int64_t)qc * p.st_q;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      u32x4_t t = qi < T ? *reinterpret_cast<const u32x4_t*>(qrow + ks * 16 + lhalf * 8)
-                         : u32x4_t{0, 0, 0, 0};
-      qf[ks] = __builtin_bit_cast(bf16x8_t, t);
-    }
+    for (int ks = 0; ks < 4; ++ks)
+      qf[ks] = __builtin_bit_cast(bf16x8_t,
+                                  *reinterpret_cast<const u32x4_t*>(qrow + ks * 16 + lhalf * 8));
   }
 
-  // K/V tile staging: thread -> (key, 16-byte chunk) for two chunks each of K and V
+  // K/V tile staging: thread -> (key, 16-byte chunk), two chunks each of K and V.
+  // Keys past T load key T-1 (masked: a key >= T is never visible).
   u32x4_t rk[2], rv[2];
   auto gload = [&](int t) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int id2 = tid + 256 * i, key = id2 >> 3, c = id2 & 7;
-      const int64_t kk = (int64_t)t * BKV + key;
-      if (kk < T) {
-        rk[i] = *reinterpret_cast<const u32x4_t*>(kbase + kk * p.st_k + c * 8);
-        rv[i] = *reinterpret_cast<const u32x4_t*>(vbase + kk * p.st_v + c * 8);
-      } else {
-        rk[i] = u32x4_t{0, 0, 0, 0};
-        rv[i] = u32x4_t{0, 0, 0, 0};
-      }
+      int kk = t * BKV + key;
+      kk = kk < T ? kk : T - 1;
+      rk[i] = *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)kk * p.st_k + c * 8);
+      rv[i] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)kk * p.st_v + c * 8);
     }
   };
   auto sstore = [&](int stage) {
@@ -112,11 +112,16 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
     for (int i = 0; i < 2; ++i) {
       const int id2 = tid + 256 * i, key = id2 >> 3, c = id2 & 7;
       *reinterpret_cast<u32x4_t*>(sk + kswz(key, c)) = rk[i];
-      const uint16_t* e = reinterpret_cast<const uint16_t*>(&rv[i]);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sv[(c * 8 + j) * VT_LD + key] = e[j];
+      *reinterpret_cast<u32x4_t*>(sv + key * V_LD + c * 8) = rv[i];
     }
   };
+
+  // Transposing V reads: in each 16-lane group, source lane s points at
+  // V[k0 + 4*lhalf + s/4][dcol + 4*(s%4)], so lane t of the group receives
+  // V[k0 + 4*lhalf + e][dcol + t], e = 0..3 (t = lane % 16, dcol covers 16
+  // columns per group: 16 * ((lane >> 4) & 1) within the 32-column half).
+  const int s16 = lane & 15;
+  const int vt_lane = (4 * lhalf + (s16 >> 2)) * V_LD + 16 * ((lane >> 4) & 1) + 4 * (s16 & 3);
 
   f32x16_t o[2];
 #pragma unroll
@@ -136,7 +141,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
     if (wave_active && t >= wt_begin && t <= wt_end) {
       const uint16_t* sk = lds + stage * STAGE;
       const uint16_t* sv = sk + K_TILE;
-      const int64_t kb = (int64_t)t * BKV;
+      const int kb = t * BKV;
       // ---- S^T = K . Q^T (two 32-key sub-tiles) ----
       f32x16_t s[2];
 #pragma unroll
@@ -157,16 +162,14 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
       const bool need_mask = (p.causal && kb + BKV - 1 > qw) ||
                              (window > 0 && kb <= qw + 31 - window) || (kb + BKV > T);
       if (need_mask) {
+        const int lim_hi = p.causal ? (qi < T - 1 ? qi : T - 1) : T - 1;  // key <= lim_hi
+        const int lim_lo = window > 0 ? qi - window : -1;                  // key > lim_lo
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int64_t key = kb + sub * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-            bool vis = key < T;
-            if (p.causal) {
-              vis = vis && key <= qi;
-              if (window > 0) vis = vis && key > qi - window;
-            }
+            const int key = kb + sub * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+            const bool vis = (key <= lim_hi) & (key > lim_lo);
             s[sub][r] = vis ? s[sub][r] : -INFINITY;
           }
       }
@@ -178,7 +181,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
       mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * sl2;
       if (__any(mt > m + 8.f)) {
         const float m_new = fmaxf(m, mt);
-        const float alpha = m_new == -INFINITY ? 1.f : exp2f(m - m_new);
+        const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - m_new);
         m = m_new;
         l *= alpha;
 #pragma unroll
@@ -196,8 +199,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
           uint32_t w[4];
 #pragma unroll
           for (int e = 0; e < 8; e += 2) {
-            const float p0 = exp2f(fmaf(s[sub][8 * u + e], sl2, -m_use));
-            const float p1 = exp2f(fmaf(s[sub][8 * u + e + 1], sl2, -m_use));
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(s[sub][8 * u + e], sl2, -m_use));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(s[sub][8 * u + e + 1], sl2, -m_use));
             ls += p0 + p1;
             w[e >> 1] = pack_bf16x2(p0, p1);
           }
@@ -206,19 +209,19 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
       l += ls;
       // ---- O^T += V^T . P^T ----
 #pragma unroll
-      for (int dsub = 0; dsub < 2; ++dsub) {
-        const uint16_t* vrow = sv + (dsub * 32 + lrow) * VT_LD;
+      for (int dsub = 0; dsub < 2; ++dsub)
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
-            const int k0 = sub * 32 + u * 16 + 4 * lhalf;
-            const u32x2_t lo4 = *reinterpret_cast<const u32x2_t*>(vrow + k0);
-            const u32x2_t hi4 = *reinterpret_cast<const u32x2_t*>(vrow + k0 + 8);
-            const bf16x8_t a = __builtin_bit_cast(bf16x8_t, u32x4_t{lo4.x, lo4.y, hi4.x, hi4.y});
+            const uint16_t* vp = sv + (sub * 32 + u * 16) * V_LD + dsub * 32 + vt_lane;
+            const s16x4_t t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(vp));
+            const s16x4_t t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(vp + 8 * V_LD));
+            const u32x2_t w0 = __builtin_bit_cast(u32x2_t, t0);
+            const u32x2_t w1 = __builtin_bit_cast(u32x2_t, t1);
+            const bf16x8_t a = __builtin_bit_cast(bf16x8_t, u32x4_t{w0.x, w0.y, w1.x, w1.y});
             o[dsub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[sub][u], o[dsub], 0, 0, 0);
           }
-      }
     }
     if (t < t_end) sstore((t + 1 - t_begin) & 1);
     __syncthreads();
@@ -227,7 +230,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
   if (!wave_active || qi >= T) return;
   const float lt = l + __shfl_xor(l, 32, 64);
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
-  uint16_t* orow = p.o + b * p.sb_o + h * p.sh_o + qi * p.st_o;
+  uint16_t* orow = p.o + b * p.sb_o + h * p.sh_o + (int64_t)qi * p.st_o;
 #pragma unroll
   for (int dsub = 0; dsub < 2; ++dsub)
 #pragma unroll
@@ -244,6 +247,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
 
 int launch_attention(const AttnArgs& a, hipStream_t s) {
   if (a.B == 0 || a.H == 0 || a.T == 0) return 0;
+  if (a.T > 0x3fffffff) return fail(-2, "attention: T too large");
   const int64_t nb = ((a.T + BQ - 1) / BQ) * a.H * a.B;
   if (nb > 0x7fffffff) return fail(-2, "attention: grid too large");
   hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)nb), dim3(256), 0, s, a);
