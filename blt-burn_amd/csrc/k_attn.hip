@@ -1,8 +1,8 @@
 // Causal (optionally sliding-window) attention for gfx950, head_dim 64, bf16
 // operands on MFMA, f32 online softmax.
 //
-// One block = 4 wave64s = 128 queries of one (batch, head); K/V advance in
-// 64-key tiles through two LDS stages shared by the four waves.
+// One block = 4 wave64s = 128 or 256 queries of one (batch, head); K/V
+// advance in 64-key tiles through two LDS stages shared by the four waves.
 //
 // Each wave computes S^T = K . Q^T (v_mfma_f32_32x32x16_bf16, keys as rows,
 // its 32 queries as columns), so a lane owns one query column and 32 of the
@@ -24,7 +24,6 @@ namespace blt {
 
 namespace {
 
-constexpr int BQ = 128;     // queries per block
 constexpr int BKV = 64;     // keys per tile
 constexpr int D = 64;       // head dim
 constexpr int V_LD = 72;    // V row pitch in bf16 (144 B): conflict-free transposing reads
@@ -39,7 +38,12 @@ typedef short s16x4_t __attribute__((ext_vector_type(4)));
 // 16 rows one LDS cycle serves for an operand load fall in 16 distinct banks.
 __device__ inline int kswz(int key, int chunk) { return key * D + ((chunk ^ ((key >> 1) & 7)) << 3); }
 
+// NQ 32-query column blocks per wave (QPW = 32 * NQ queries); each K and V^T
+// fragment read from LDS feeds NQ MFMAs.  Block = 4 waves = 4 * QPW queries.
+template <int NQ>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
+  constexpr int QPW = 32 * NQ;
+  constexpr int BQ = 4 * QPW;
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -58,7 +62,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
   const int64_t h = bh % p.H, b = bh / p.H;
 
   const int q0 = qb * BQ;
-  const int qw = q0 + wid * 32;  // this wave's first query
+  const int qw = q0 + wid * QPW;  // this wave's first query
   const int window = p.causal ? p.window : 0;
 
   // block key range
@@ -71,7 +75,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
   // wave key range
   int wlo = 0, whi = T - 1;
   if (p.causal) {
-    whi = qw + 31 < T - 1 ? qw + 31 : T - 1;
+    whi = qw + QPW - 1 < T - 1 ? qw + QPW - 1 : T - 1;
     if (window > 0) wlo = qw - window + 1 > 0 ? qw - window + 1 : 0;
   }
   const bool wave_active = qw < T;
@@ -80,16 +84,18 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
   const uint16_t* kbase = p.k + b * p.sb_k + h * p.sh_k;
   const uint16_t* vbase = p.v + b * p.sb_v + h * p.sh_v;
 
-  // Q fragments (B operand of S^T = K . Q^T): query qw + lrow, d = 16*ks + 8*lhalf .. +8
-  const int qi = qw + lrow;
-  bf16x8_t qf[4];
-  {
+  // Q fragments (B operand of S^T = K . Q^T): query qw + 32*qq + lrow,
+  // d = 16*ks + 8*lhalf .. +8
+  bf16x8_t qf[NQ][4];
+#pragma unroll
+  for (int qq = 0; qq < NQ; ++qq) {
+    const int qi = qw + 32 * qq + lrow;
     const int qc = qi < T ? qi : T - 1;  // rows past T load a valid row, never stored
     const uint16_t* qrow = p.q + b * p.sb_q + h * p.sh_q + (int64_t)qc * p.st_q;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
-      qf[ks] = __builtin_bit_cast(bf16x8_t,
-                                  *reinterpret_cast<const u32x4_t*>(qrow + ks * 16 + lhalf * 8));
+      qf[qq][ks] = __builtin_bit_cast(
+          bf16x8_t, *reinterpret_cast<const u32x4_t*>(qrow + ks * 16 + lhalf * 8));
   }
 
   // K/V tile staging: thread -> (key, 16-byte chunk), two chunks each of K and V.
@@ -123,12 +129,17 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
   const int s16 = lane & 15;
   const int vt_lane = (4 * lhalf + (s16 >> 2)) * V_LD + 16 * ((lane >> 4) & 1) + 4 * (s16 & 3);
 
-  f32x16_t o[2];
+  f32x16_t o[NQ][2];
+  float m[NQ], l[NQ];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int qq = 0; qq < NQ; ++qq) {
+    m[qq] = -INFINITY;
+    l[qq] = 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[j][r] = 0.f;
-  float m = -INFINITY, l = 0.f;
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[qq][j][r] = 0.f;
+  }
   const float sl2 = 0.125f * 1.44269504088896340736f;  // 1/sqrt(64) * log2(e)
 
   gload(t_begin);
@@ -142,71 +153,81 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
       const uint16_t* sk = lds + stage * STAGE;
       const uint16_t* sv = sk + K_TILE;
       const int kb = t * BKV;
-      // ---- S^T = K . Q^T (two 32-key sub-tiles) ----
-      f32x16_t s[2];
+      // ---- S^T = K . Q^T (two 32-key sub-tiles x NQ query blocks) ----
+      f32x16_t s[NQ][2];
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
+      for (int qq = 0; qq < NQ; ++qq)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[sub][r] = 0.f;
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[qq][sub][r] = 0.f;
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
           const bf16x8_t a =
               *reinterpret_cast<const bf16x8_t*>(sk + kswz(sub * 32 + lrow, ks * 2 + lhalf));
-          s[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], s[sub], 0, 0, 0);
+#pragma unroll
+          for (int qq = 0; qq < NQ; ++qq)
+            s[qq][sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[qq][ks], s[qq][sub], 0, 0, 0);
         }
-      }
       // ---- mask, online softmax (log2 domain, scale folded into one FMA) ----
       // The running max used for exponentiation (m) only moves when a row's
       // max grows by more than 2^8 (checked wave-wide), so P <= 256 and the
       // O / l rescale is skipped for most tiles; O / l is unchanged by it.
       const bool need_mask = (p.causal && kb + BKV - 1 > qw) ||
-                             (window > 0 && kb <= qw + 31 - window) || (kb + BKV > T);
-      if (need_mask) {
-        const int lim_hi = p.causal ? (qi < T - 1 ? qi : T - 1) : T - 1;  // key <= lim_hi
-        const int lim_lo = window > 0 ? qi - window : -1;                  // key > lim_lo
+                             (window > 0 && kb <= qw + QPW - 1 - window) || (kb + BKV > T);
+      bf16x8_t pb[NQ][2][2];
+#pragma unroll
+      for (int qq = 0; qq < NQ; ++qq) {
+        const int qi = qw + 32 * qq + lrow;
+        if (need_mask) {
+          const int lim_hi = p.causal ? (qi < T - 1 ? qi : T - 1) : T - 1;  // key <= lim_hi
+          const int lim_lo = window > 0 ? qi - window : -1;                  // key > lim_lo
+#pragma unroll
+          for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int key = kb + sub * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+              const bool vis = (key <= lim_hi) & (key > lim_lo);
+              s[qq][sub][r] = vis ? s[qq][sub][r] : -INFINITY;
+            }
+        }
+        float mt = -INFINITY;
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = kb + sub * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-            const bool vis = (key <= lim_hi) & (key > lim_lo);
-            s[sub][r] = vis ? s[sub][r] : -INFINITY;
-          }
-      }
-      float mt = -INFINITY;
+          for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[qq][sub][r]);
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * sl2;
+        if (__any(mt > m[qq] + 8.f)) {
+          const float m_new = fmaxf(m[qq], mt);
+          const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[qq] - m_new);
+          m[qq] = m_new;
+          l[qq] *= alpha;
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
+          for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[sub][r]);
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * sl2;
-      if (__any(mt > m + 8.f)) {
-        const float m_new = fmaxf(m, mt);
-        const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - m_new);
-        m = m_new;
-        l *= alpha;
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
-      }
-      const float m_use = m == -INFINITY ? 0.f : m;
-      float ls = 0.f;
-      bf16x8_t pb[2][2];
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          uint32_t w[4];
-#pragma unroll
-          for (int e = 0; e < 8; e += 2) {
-            const float p0 = __builtin_amdgcn_exp2f(fmaf(s[sub][8 * u + e], sl2, -m_use));
-            const float p1 = __builtin_amdgcn_exp2f(fmaf(s[sub][8 * u + e + 1], sl2, -m_use));
-            ls += p0 + p1;
-            w[e >> 1] = pack_bf16x2(p0, p1);
-          }
-          pb[sub][u] = __builtin_bit_cast(bf16x8_t, u32x4_t{w[0], w[1], w[2], w[3]});
+            for (int r = 0; r < 16; ++r) o[qq][j][r] *= alpha;
         }
-      l += ls;
+        const float m_use = m[qq] == -INFINITY ? 0.f : m[qq];
+        float ls = 0.f;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+              const float p0 = __builtin_amdgcn_exp2f(fmaf(s[qq][sub][8 * u + e], sl2, -m_use));
+              const float p1 =
+                  __builtin_amdgcn_exp2f(fmaf(s[qq][sub][8 * u + e + 1], sl2, -m_use));
+              ls += p0 + p1;
+              w[e >> 1] = pack_bf16x2(p0, p1);
+            }
+            pb[qq][sub][u] = __builtin_bit_cast(bf16x8_t, u32x4_t{w[0], w[1], w[2], w[3]});
+          }
+        l[qq] += ls;
+      }
       // ---- O^T += V^T . P^T ----
 #pragma unroll
       for (int dsub = 0; dsub < 2; ++dsub)
@@ -220,27 +241,45 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
             const u32x2_t w0 = __builtin_bit_cast(u32x2_t, t0);
             const u32x2_t w1 = __builtin_bit_cast(u32x2_t, t1);
             const bf16x8_t a = __builtin_bit_cast(bf16x8_t, u32x4_t{w0.x, w0.y, w1.x, w1.y});
-            o[dsub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[sub][u], o[dsub], 0, 0, 0);
+#pragma unroll
+            for (int qq = 0; qq < NQ; ++qq)
+              o[qq][dsub] =
+                  __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[qq][sub][u], o[qq][dsub], 0, 0, 0);
           }
     }
     if (t < t_end) sstore((t + 1 - t_begin) & 1);
     __syncthreads();
   }
 
-  if (!wave_active || qi >= T) return;
-  const float lt = l + __shfl_xor(l, 32, 64);
-  const float inv = lt > 0.f ? 1.f / lt : 0.f;
-  uint16_t* orow = p.o + b * p.sb_o + h * p.sh_o + (int64_t)qi * p.st_o;
+  if (!wave_active) return;
 #pragma unroll
-  for (int dsub = 0; dsub < 2; ++dsub)
+  for (int qq = 0; qq < NQ; ++qq) {
+    const int qi = qw + 32 * qq + lrow;
+    if (qi >= T) continue;
+    const float lt = l[qq] + __shfl_xor(l[qq], 32, 64);
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    uint16_t* orow = p.o + b * p.sb_o + h * p.sh_o + (int64_t)qi * p.st_o;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d0 = dsub * 32 + 8 * j + 4 * lhalf;
-      u32x2_t w;
-      w.x = pack_bf16x2(o[dsub][4 * j] * inv, o[dsub][4 * j + 1] * inv);
-      w.y = pack_bf16x2(o[dsub][4 * j + 2] * inv, o[dsub][4 * j + 3] * inv);
-      *reinterpret_cast<u32x2_t*>(orow + d0) = w;
-    }
+    for (int dsub = 0; dsub < 2; ++dsub)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d0 = dsub * 32 + 8 * j + 4 * lhalf;
+        u32x2_t w;
+        w.x = pack_bf16x2(o[qq][dsub][4 * j] * inv, o[qq][dsub][4 * j + 1] * inv);
+        w.y = pack_bf16x2(o[qq][dsub][4 * j + 2] * inv, o[qq][dsub][4 * j + 3] * inv);
+        *reinterpret_cast<u32x2_t*>(orow + d0) = w;
+      }
+  }
+}
+
+template <int NQ>
+int run_attention(const AttnArgs& a, hipStream_t s) {
+  constexpr int BQ = 4 * 32 * NQ;
+  const int64_t nb = ((a.T + BQ - 1) / BQ) * a.H * a.B;
+  if (nb > 0x7fffffff) return fail(-2, "attention: grid too large");
+  hipLaunchKernelGGL((attn_fwd_kernel<NQ>), dim3((unsigned)nb), dim3(256), 0, s, a);
+  BLT_LAUNCH_CHECK("attn_fwd_kernel");
+  return 0;
 }
 
 }  // namespace
@@ -248,11 +287,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
 int launch_attention(const AttnArgs& a, hipStream_t s) {
   if (a.B == 0 || a.H == 0 || a.T == 0) return 0;
   if (a.T > 0x3fffffff) return fail(-2, "attention: T too large");
-  const int64_t nb = ((a.T + BQ - 1) / BQ) * a.H * a.B;
-  if (nb > 0x7fffffff) return fail(-2, "attention: grid too large");
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)nb), dim3(256), 0, s, a);
-  BLT_LAUNCH_CHECK("attn_fwd_kernel");
-  return 0;
+  // 64 queries per wave (1 wave per SIMD) pays off for long full-causal rows;
+  // with a window, 32 queries per wave (2 waves per SIMD) wastes less of
+  // each masked band tile and hides latency better.
+  const bool full_causal = a.causal && (a.window == 0 || a.window >= a.T);
+  if (full_causal && a.T >= 2048 && a.T * a.H * a.B >= 256 * 256 * 4)
+    return run_attention<2>(a, s);
+  return run_attention<1>(a, s);
 }
 
 }  // namespace blt
