@@ -46,6 +46,12 @@ EXPORTS = {
     "blt_model_destroy": (c_i32, [c_vp]),
     "blt_model_device_bytes": (c_i64, [c_vp]),
     "blt_model_forward": (c_i32, [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp]),
+    "blt_model_forward_segments": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp]),
+    "blt_tokenize_bytes": (c_i32, [c_vp, c_i64, c_i32, c_i32, c_vp, c_i64, c_vp]),
+    "blt_ingest_plan_chunks": (c_i32, [c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i64]),
+    "blt_ingest_create": (c_i32, [c_vp, c_vp, c_vp]),
+    "blt_ingest_destroy": (c_i32, [c_vp]),
+    "blt_ingest_run": (c_i32, [c_vp, c_vp, c_vp, c_i64] + [c_vp] * 7),
     "blt_model_set_profiling": (c_i32, [c_vp, c_i32]),
     "blt_model_read_profile": (c_i32, [c_vp, ctypes.POINTER(c_f64), ctypes.POINTER(c_i64), c_i32]),
     "blt_stage_name": (ctypes.c_char_p, [c_i32]),
@@ -82,6 +88,12 @@ OUTPUT_FIELDS = ("logits", "pre_norm_embeddings", "embedding_norms", "entropies"
 
 class ModelOutputs(ctypes.Structure):
     _fields_ = [(n, c_vp) for n in OUTPUT_FIELDS]
+
+
+class IngestConfig(ctypes.Structure):
+    """blt_ingest_config."""
+    _fields_ = [("rows", c_i32), ("row_len", c_i32), ("chunk_len", c_i32), ("overlap", c_i32),
+                ("threshold", c_f32), ("mode", c_i32), ("with_embeddings", c_i32)]
 
 
 _lib = None

@@ -295,6 +295,15 @@ int blt_model_forward(blt_model* m, const int32_t* tokens, int64_t B, int64_t T,
   return reinterpret_cast<Model*>(m)->forward(tokens, B, T, *out, STREAM(stream));
 }
 
+int blt_model_forward_segments(blt_model* m, const int32_t* tokens, const int32_t* seg_start,
+                               int64_t B, int64_t T, const blt_model_outputs* out,
+                               blt_stream_t stream) {
+  if (!m || !out) return fail(BLT_ERR_INVALID, "model_forward_segments: null argument");
+  if (!seg_start && B * T > 0)
+    return fail(BLT_ERR_INVALID, "model_forward_segments: null seg_start");
+  return reinterpret_cast<Model*>(m)->forward(tokens, B, T, *out, STREAM(stream), seg_start);
+}
+
 int blt_model_set_profiling(blt_model* m, int32_t on) {
   if (!m) return fail(BLT_ERR_INVALID, "model_set_profiling: null model");
   reinterpret_cast<Model*>(m)->profiling = on != 0;

@@ -63,6 +63,16 @@ struct GemmCfg {
 // + r % 4: each lane owns one output row and 4 consecutive columns per
 // register group, which the epilogues store as one 8-byte (bf16) or 16-byte
 // (f32) vector.
+// RoPE position of output row `row` (a token of a [B, seq_len] batch): its
+// index in the row, minus its segment's start when rows are packed.
+__device__ inline int64_t rope_pos(const GemmArgs& p, int64_t row) {
+  const int64_t t = row % p.seq_len;
+  if (!p.seg_start) return t;
+  int64_t s = p.seg_start[row < p.M ? row : p.M - 1];
+  s = s < 0 ? 0 : (s > t ? t : s);
+  return t - s;
+}
+
 template <class C>
 __device__ inline void epilogue(const GemmArgs& p, f32x16_t (&acc)[C::TM][C::TN], int64_t m0,
                                 int64_t n0, int wm, int wn, int lrow, int lhalf) {
@@ -75,7 +85,7 @@ __device__ inline void epilogue(const GemmArgs& p, f32x16_t (&acc)[C::TM][C::TN]
     for (int i = 0; i < C::TM; ++i) {
       const int64_t row = row_base + i * 32;
       if (row >= p.M) continue;
-      const int64_t pos = p.epi == EPI_QKV_ROPE ? row % p.seq_len : 0;
+      const int64_t pos = p.epi != EPI_QKV_ROPE ? 0 : rope_pos(p, row);
 #pragma unroll
       for (int j = 0; j < C::TN; j += 2)
 #pragma unroll
@@ -370,7 +380,7 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
       const int i = i0 + ii;
       const int rl = ii * 32 + lrow;  // row within this 64-row slab
       const int64_t row = row0 + i * 32 + lrow;
-      const int64_t pos = p.epi == EPI_QKV_ROPE ? row % p.seq_len : 0;
+      const int64_t pos = p.epi != EPI_QKV_ROPE ? 0 : rope_pos(p, row);
       if (p.epi == EPI_BF16) {
 #pragma unroll
         for (int j = 0; j < C::TN; ++j)

@@ -1,0 +1,440 @@
+// Streaming ingest: token documents -> per-document entropies, pre-norm
+// embedding norms, coherence, (optionally) pre-norm embeddings and patch
+// boundaries, through the packed-row entropy-model forward.  Also the host
+// byte tokenizer that produces those token documents.
+//
+// Reference semantics (blt_core.rs:286-370, compute_all_signals_chunked): a
+// document longer than one model sequence is cut into chunks of at most
+// `chunk_len` tokens; the first chunk is [0, stride), every later chunk
+// starts `overlap` tokens before the current position and its first
+// `overlap` outputs are dropped (stride = chunk_len - overlap).  Each chunk is
+// an independent forward; the document's stitched entropies then go through
+// the boundary pass (blt_core.rs:182-199, patcher.rs:80-164) and coherence
+// n^2 / (H + 1e-6) (blt_core.rs:202-207).
+//
+// Here the chunks of many documents are packed into [rows, row_len] batches
+// (per-segment attention and RoPE positions keep every chunk independent, as
+// the reference's one-chunk-per-forward loop does), and a whole document
+// always lands in one batch so its boundary pass runs on the device right
+// after the forward.  Host packing of batch i+1 overlaps the GPU work of
+// batch i: two slots of pinned host + device buffers, uploads on one stream,
+// the model on a compute stream, downloads on a third, events between them.
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "model.hpp"
+
+namespace blt {
+
+struct ChunkPlan {
+  int64_t start;  // first token of the chunk in the document
+  int32_t len;    // tokens in the chunk
+  int32_t skip;   // leading outputs that are overlap context (dropped)
+};
+
+// blt_core.rs:300-356.  With 2 * overlap <= chunk_len (checked by callers)
+// every later chunk starts exactly `overlap` tokens before the current
+// position, so kept output j of a chunk is document token start + j.
+static void plan_chunks(int64_t L, int64_t chunk, int64_t overlap, std::vector<ChunkPlan>& out) {
+  out.clear();
+  const int64_t stride = chunk - overlap;
+  int64_t pos = 0;
+  while (pos < L) {
+    const int64_t start = pos == 0 ? 0 : pos - overlap;
+    const int64_t end = std::min(pos + stride, L);
+    out.push_back({start, (int32_t)(end - start), (int32_t)(pos - start)});
+    pos = end;
+  }
+}
+
+// First-fit, longest chunk first, into rows of capacity T with current fill.
+// On success fill is updated and row/col give each chunk's place.
+static bool pack_chunks(const std::vector<ChunkPlan>& c, std::vector<int64_t>& fill, int64_t T,
+                        std::vector<int>& order, std::vector<int64_t>& row,
+                        std::vector<int64_t>& col) {
+  const int64_t B = (int64_t)fill.size();
+  order.resize(c.size());
+  for (size_t i = 0; i < c.size(); ++i) order[i] = (int)i;
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return c[a].len > c[b].len; });
+  row.assign(c.size(), -1);
+  col.assign(c.size(), 0);
+  std::vector<int64_t> trial = fill;
+  for (int ci : order) {
+    int64_t r = 0;
+    while (r < B && trial[r] + c[ci].len > T) ++r;
+    if (r == B) return false;
+    row[ci] = r;
+    col[ci] = trial[r];
+    trial[r] += c[ci].len;
+  }
+  fill.swap(trial);
+  return true;
+}
+
+struct Ingest {
+  Model* m = nullptr;
+  blt_ingest_config cfg{};
+  int64_t BT = 0, dim = 0;
+  hipStream_t up = nullptr, ks = nullptr, down = nullptr;
+
+  struct Slot {
+    // pinned host
+    int32_t* h_tok = nullptr;
+    int32_t* h_seg = nullptr;
+    int32_t* h_dest = nullptr;
+    int64_t* h_doff = nullptr;
+    int32_t* h_dlen = nullptr;
+    float* h_H = nullptr;
+    float* h_N = nullptr;
+    float* h_C = nullptr;
+    float* h_E = nullptr;
+    int32_t* h_starts = nullptr;
+    int32_t* h_lens = nullptr;
+    int32_t* h_counts = nullptr;
+    // device
+    int32_t* d_tok = nullptr;
+    int32_t* d_seg = nullptr;
+    int32_t* d_dest = nullptr;
+    int64_t* d_doff = nullptr;
+    int32_t* d_dlen = nullptr;
+    float* d_Hp = nullptr;  // packed-row outputs
+    float* d_Np = nullptr;
+    float* d_Cp = nullptr;
+    float* d_Ep = nullptr;
+    float* d_H = nullptr;   // document order
+    float* d_N = nullptr;
+    float* d_C = nullptr;
+    float* d_E = nullptr;
+    int32_t* d_starts = nullptr;
+    int32_t* d_lens = nullptr;
+    int32_t* d_counts = nullptr;
+    hipEvent_t uploaded = nullptr, computed = nullptr, done = nullptr;
+    bool busy = false;
+    std::vector<int64_t> docs;  // caller's document ids in this batch
+    int64_t out_tokens = 0;     // tokens of those documents
+  } slot[2];
+
+  ~Ingest();
+  int init(Model* model, const blt_ingest_config& c);
+  int run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, float* ent, float* nrm,
+          float* coh, float* emb, int32_t* starts, int32_t* lens, int32_t* counts);
+  int finish(Slot& s, const int64_t* doc_off, float* ent, float* nrm, float* coh, float* emb,
+             int32_t* starts, int32_t* lens, int32_t* counts);
+};
+
+Ingest::~Ingest() {
+  for (Slot& s : slot) {
+    if (s.busy && s.done) (void)hipEventSynchronize(s.done);
+    void* hp[] = {s.h_tok, s.h_seg, s.h_dest, s.h_doff,   s.h_dlen, s.h_H,
+                  s.h_N,   s.h_C,   s.h_E,    s.h_starts, s.h_lens, s.h_counts};
+    for (void* p : hp)
+      if (p) (void)hipHostFree(p);
+    void* dp[] = {s.d_tok, s.d_seg, s.d_dest, s.d_doff, s.d_dlen,   s.d_Hp,   s.d_Np,
+                  s.d_Cp,  s.d_Ep,  s.d_H,    s.d_N,    s.d_C,      s.d_E,    s.d_starts,
+                  s.d_lens, s.d_counts};
+    for (void* p : dp)
+      if (p) (void)hipFree(p);
+    for (hipEvent_t e : {s.uploaded, s.computed, s.done})
+      if (e) (void)hipEventDestroy(e);
+  }
+  for (hipStream_t st : {up, ks, down})
+    if (st) (void)hipStreamDestroy(st);
+}
+
+int Ingest::init(Model* model, const blt_ingest_config& c) {
+  m = model;
+  cfg = c;
+  if (cfg.chunk_len == 0) cfg.chunk_len = cfg.row_len;
+  if (cfg.rows <= 0 || cfg.row_len <= 0 || cfg.chunk_len <= 0 || cfg.chunk_len > cfg.row_len)
+    return fail(BLT_ERR_SHAPE, "ingest: rows > 0, 0 < chunk_len <= row_len");
+  if (cfg.overlap < 0 || 2 * (int64_t)cfg.overlap > cfg.chunk_len)
+    return fail(BLT_ERR_SHAPE,
+                "ingest: 0 <= overlap and 2 * overlap <= chunk_len (with a larger overlap the "
+                "reference chunk loop misplaces outputs)");
+  if (cfg.row_len > m->cfg.max_seqlen) return fail(BLT_ERR_SHAPE, "ingest: row_len > max_seqlen");
+  if (cfg.mode != BLT_PATCH_MONOTONIC && cfg.mode != BLT_PATCH_GLOBAL)
+    return fail(BLT_ERR_INVALID, "ingest: bad patch mode");
+  BT = (int64_t)cfg.rows * cfg.row_len;
+  dim = m->cfg.dim;
+  if (BT > m->max_tokens) return fail(BLT_ERR_SHAPE, "ingest: rows * row_len > model max_tokens");
+  if (BT > 0x7fffffff) return fail(BLT_ERR_SHAPE, "ingest: rows * row_len >= 2^31");
+  BLT_HIP_CHECK(hipSetDevice(m->device));
+  BLT_HIP_CHECK(hipStreamCreateWithFlags(&up, hipStreamNonBlocking));
+  BLT_HIP_CHECK(hipStreamCreateWithFlags(&ks, hipStreamNonBlocking));
+  BLT_HIP_CHECK(hipStreamCreateWithFlags(&down, hipStreamNonBlocking));
+  const int64_t ne = cfg.with_embeddings ? BT * dim : 0;
+  for (Slot& s : slot) {
+#define HALLOC(p, n) \
+  if (n) BLT_HIP_CHECK(hipHostMalloc((void**)&(p), (size_t)(n) * sizeof(*(p)), 0))
+#define DALLOC(p, n) \
+  if (n) BLT_HIP_CHECK(hipMalloc((void**)&(p), (size_t)(n) * sizeof(*(p))))
+    HALLOC(s.h_tok, BT); HALLOC(s.h_seg, BT); HALLOC(s.h_dest, BT);
+    HALLOC(s.h_doff, BT); HALLOC(s.h_dlen, BT);
+    HALLOC(s.h_H, BT); HALLOC(s.h_N, BT); HALLOC(s.h_C, BT); HALLOC(s.h_E, ne);
+    HALLOC(s.h_starts, BT); HALLOC(s.h_lens, BT); HALLOC(s.h_counts, BT);
+    DALLOC(s.d_tok, BT); DALLOC(s.d_seg, BT); DALLOC(s.d_dest, BT);
+    DALLOC(s.d_doff, BT); DALLOC(s.d_dlen, BT);
+    DALLOC(s.d_Hp, BT); DALLOC(s.d_Np, BT); DALLOC(s.d_Cp, BT); DALLOC(s.d_Ep, ne);
+    DALLOC(s.d_H, BT); DALLOC(s.d_N, BT); DALLOC(s.d_C, BT); DALLOC(s.d_E, ne);
+    DALLOC(s.d_starts, BT); DALLOC(s.d_lens, BT); DALLOC(s.d_counts, BT);
+#undef HALLOC
+#undef DALLOC
+    BLT_HIP_CHECK(hipEventCreateWithFlags(&s.uploaded, hipEventDisableTiming));
+    BLT_HIP_CHECK(hipEventCreateWithFlags(&s.computed, hipEventDisableTiming));
+    BLT_HIP_CHECK(hipEventCreateWithFlags(&s.done, hipEventDisableTiming));
+  }
+  return 0;
+}
+
+// Wait for a slot's batch and copy its per-document results to the caller.
+int Ingest::finish(Slot& s, const int64_t* doc_off, float* ent, float* nrm, float* coh,
+                   float* emb, int32_t* starts, int32_t* lens, int32_t* counts) {
+  if (!s.busy) return 0;
+  s.busy = false;
+  BLT_HIP_CHECK(hipEventSynchronize(s.done));
+  for (size_t j = 0; j < s.docs.size(); ++j) {
+    const int64_t d = s.docs[j];
+    const int64_t L = doc_off[d + 1] - doc_off[d];
+    const int64_t src = s.h_doff[j], dst = doc_off[d];
+    const int32_t n = s.h_counts[j];
+    if (ent) memcpy(ent + dst, s.h_H + src, (size_t)L * 4);
+    if (nrm) memcpy(nrm + dst, s.h_N + src, (size_t)L * 4);
+    if (coh) memcpy(coh + dst, s.h_C + src, (size_t)L * 4);
+    if (emb && s.h_E) memcpy(emb + dst * dim, s.h_E + src * dim, (size_t)(L * dim) * 4);
+    if (starts) memcpy(starts + dst, s.h_starts + src, (size_t)n * 4);
+    if (lens) memcpy(lens + dst, s.h_lens + src, (size_t)n * 4);
+    if (counts) counts[d] = n;
+  }
+  return 0;
+}
+
+int Ingest::run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, float* ent,
+                float* nrm, float* coh, float* emb, int32_t* starts, int32_t* lens,
+                int32_t* counts) {
+  if (emb && !cfg.with_embeddings)
+    return fail(BLT_ERR_INVALID, "ingest_run: embeddings asked of an ingest made without them");
+  const int64_t T = cfg.row_len, B = cfg.rows;
+  std::vector<ChunkPlan> chunks;
+  std::vector<int> order;
+  std::vector<int64_t> row, col, fill(B);
+  // every document must fit an empty batch (checked before any work is queued)
+  for (int64_t d = 0; d < n_docs; ++d) {
+    const int64_t L = doc_off[d + 1] - doc_off[d];
+    if (L < 0) return fail(BLT_ERR_SHAPE, "ingest_run: doc_offsets must be non-decreasing");
+    plan_chunks(L, cfg.chunk_len, cfg.overlap, chunks);
+    std::fill(fill.begin(), fill.end(), 0);
+    if (!pack_chunks(chunks, fill, T, order, row, col))
+      return fail(BLT_ERR_SHAPE, "ingest_run: document " + std::to_string(d) + " of " +
+                                     std::to_string(L) + " tokens does not fit one batch");
+  }
+  BLT_HIP_CHECK(hipSetDevice(m->device));
+  int k = 0, rc;
+  int64_t d = 0;
+  while (d < n_docs) {
+    Slot& s = slot[k];
+    if ((rc = finish(s, doc_off, ent, nrm, coh, emb, starts, lens, counts))) return rc;
+    std::fill(fill.begin(), fill.end(), 0);
+    s.docs.clear();
+    s.out_tokens = 0;
+    // ---- pack whole documents until the next one does not fit ----
+    for (; d < n_docs; ++d) {
+      const int64_t L = doc_off[d + 1] - doc_off[d];
+      if (L == 0) continue;  // empty documents have no outputs (blt_core.rs:160-176)
+      plan_chunks(L, cfg.chunk_len, cfg.overlap, chunks);
+      if (!pack_chunks(chunks, fill, T, order, row, col)) break;
+      const int64_t jd = (int64_t)s.docs.size();
+      s.h_doff[jd] = s.out_tokens;
+      s.h_dlen[jd] = (int32_t)L;
+      const int32_t* src = tokens + doc_off[d];
+      for (size_t ci = 0; ci < chunks.size(); ++ci) {
+        const ChunkPlan& c = chunks[ci];
+        const int64_t base = row[ci] * T + col[ci];
+        memcpy(s.h_tok + base, src + c.start, (size_t)c.len * 4);
+        const int32_t out0 = (int32_t)(s.out_tokens + c.start);
+        for (int32_t j = 0; j < c.len; ++j) {
+          s.h_seg[base + j] = (int32_t)col[ci];
+          s.h_dest[base + j] = j < c.skip ? -1 : out0 + j;
+        }
+      }
+      s.out_tokens += L;
+      s.docs.push_back(d);
+    }
+    if (s.docs.empty()) break;  // only empty documents were left
+    // padding: every free position is its own one-token segment, output dropped
+    for (int64_t r = 0; r < B; ++r)
+      for (int64_t c = fill[r]; c < T; ++c) {
+        s.h_tok[r * T + c] = 0;
+        s.h_seg[r * T + c] = (int32_t)c;
+        s.h_dest[r * T + c] = -1;
+      }
+    const int64_t nd = (int64_t)s.docs.size();
+    // ---- upload ----
+    BLT_HIP_CHECK(hipMemcpyAsync(s.d_tok, s.h_tok, (size_t)BT * 4, hipMemcpyHostToDevice, up));
+    BLT_HIP_CHECK(hipMemcpyAsync(s.d_seg, s.h_seg, (size_t)BT * 4, hipMemcpyHostToDevice, up));
+    BLT_HIP_CHECK(hipMemcpyAsync(s.d_dest, s.h_dest, (size_t)BT * 4, hipMemcpyHostToDevice, up));
+    BLT_HIP_CHECK(hipMemcpyAsync(s.d_doff, s.h_doff, (size_t)nd * 8, hipMemcpyHostToDevice, up));
+    BLT_HIP_CHECK(hipMemcpyAsync(s.d_dlen, s.h_dlen, (size_t)nd * 4, hipMemcpyHostToDevice, up));
+    BLT_HIP_CHECK(hipEventRecord(s.uploaded, up));
+    // ---- compute: packed forward, stitch, boundary pass ----
+    BLT_HIP_CHECK(hipStreamWaitEvent(ks, s.uploaded, 0));
+    blt_model_outputs o{};
+    o.entropies = s.d_Hp;
+    o.embedding_norms = s.d_Np;
+    o.coherence_scores = s.d_Cp;
+    o.pre_norm_embeddings = s.d_Ep;  // null unless with_embeddings
+    if ((rc = m->forward(s.d_tok, B, T, o, ks, s.d_seg))) return rc;
+    if ((rc = launch_scatter_tokens(s.d_dest, s.d_Hp, s.d_Np, s.d_Cp, s.d_H, s.d_N, s.d_C, BT,
+                                    ks)))
+      return rc;
+    if (s.d_E && (rc = launch_scatter_rows(s.d_dest, s.d_Ep, s.d_E, BT, (int)dim, ks))) return rc;
+    if ((rc = launch_patch_boundaries_varlen(s.d_H, s.d_doff, s.d_dlen, nd, cfg.threshold,
+                                             cfg.mode, nullptr, s.d_starts, s.d_lens,
+                                             s.d_counts, ks)))
+      return rc;
+    BLT_HIP_CHECK(hipEventRecord(s.computed, ks));
+    // ---- download ----
+    BLT_HIP_CHECK(hipStreamWaitEvent(down, s.computed, 0));
+    const size_t ob = (size_t)s.out_tokens * 4;
+    BLT_HIP_CHECK(hipMemcpyAsync(s.h_H, s.d_H, ob, hipMemcpyDeviceToHost, down));
+    BLT_HIP_CHECK(hipMemcpyAsync(s.h_N, s.d_N, ob, hipMemcpyDeviceToHost, down));
+    BLT_HIP_CHECK(hipMemcpyAsync(s.h_C, s.d_C, ob, hipMemcpyDeviceToHost, down));
+    if (s.d_E)
+      BLT_HIP_CHECK(hipMemcpyAsync(s.h_E, s.d_E, ob * dim, hipMemcpyDeviceToHost, down));
+    BLT_HIP_CHECK(hipMemcpyAsync(s.h_starts, s.d_starts, ob, hipMemcpyDeviceToHost, down));
+    BLT_HIP_CHECK(hipMemcpyAsync(s.h_lens, s.d_lens, ob, hipMemcpyDeviceToHost, down));
+    BLT_HIP_CHECK(hipMemcpyAsync(s.h_counts, s.d_counts, (size_t)nd * 4, hipMemcpyDeviceToHost,
+                                 down));
+    BLT_HIP_CHECK(hipEventRecord(s.done, down));
+    s.busy = true;
+    k ^= 1;
+  }
+  for (Slot& s : slot)
+    if ((rc = finish(s, doc_off, ent, nrm, coh, emb, starts, lens, counts))) return rc;
+  if (counts)
+    for (int64_t dd = 0; dd < n_docs; ++dd)
+      if (doc_off[dd + 1] == doc_off[dd]) counts[dd] = 0;
+  return 0;
+}
+
+// ---- byte tokenizer ---------------------------------------------------------
+// Length of the well-formed UTF-8 sequence starting at p[0] (1..4), or 0 when
+// p[0] starts an ill-formed one; then *bad is the length of its maximal
+// subpart (the prefix of a well-formed sequence, at least 1), which
+// from_utf8_lossy replaces by one U+FFFD.  Well-formed sequences are those of
+// the Unicode Standard, Table 3-7.
+static int utf8_seq(const uint8_t* p, int64_t left, int* bad) {
+  const uint8_t b0 = p[0];
+  if (b0 < 0x80) return 1;
+  int need;
+  uint8_t lo = 0x80, hi = 0xBF;  // range of the second byte
+  if (b0 >= 0xC2 && b0 <= 0xDF) {
+    need = 2;
+  } else if (b0 >= 0xE0 && b0 <= 0xEF) {
+    need = 3;
+    if (b0 == 0xE0) lo = 0xA0;
+    if (b0 == 0xED) hi = 0x9F;
+  } else if (b0 >= 0xF0 && b0 <= 0xF4) {
+    need = 4;
+    if (b0 == 0xF0) lo = 0x90;
+    if (b0 == 0xF4) hi = 0x8F;
+  } else {
+    *bad = 1;
+    return 0;
+  }
+  int i = 1;
+  for (; i < need && i < left; ++i) {
+    const uint8_t b = p[i];
+    const uint8_t l = i == 1 ? lo : 0x80, h = i == 1 ? hi : 0xBF;
+    if (b < l || b > h) break;
+  }
+  if (i == need) return need;
+  *bad = i;
+  return 0;
+}
+
+}  // namespace blt
+
+using namespace blt;
+
+extern "C" {
+
+int blt_tokenize_bytes(const uint8_t* bytes, int64_t n, int32_t add_bos, int32_t add_eos,
+                       int32_t* tokens, int64_t cap, int64_t* n_tokens) {
+  if (n < 0 || (n > 0 && !bytes) || !n_tokens)
+    return fail(BLT_ERR_INVALID, "tokenize_bytes: bad argument");
+  const int32_t kOffset = 4, kBos = 1, kEos = 2;  // tokenizer.rs:4-8
+  int64_t w = 0;
+  auto put = [&](int32_t t) {
+    if (tokens && w < cap) tokens[w] = t;
+    ++w;
+  };
+  if (add_bos) put(kBos);
+  int64_t i = 0;
+  while (i < n) {
+    int bad = 0;
+    const int len = utf8_seq(bytes + i, n - i, &bad);
+    if (len) {
+      for (int j = 0; j < len; ++j) put((int32_t)bytes[i + j] + kOffset);
+      i += len;
+    } else {
+      put(0xEF + kOffset);
+      put(0xBF + kOffset);
+      put(0xBD + kOffset);
+      i += bad;
+    }
+  }
+  if (add_eos) put(kEos);
+  *n_tokens = w;
+  if (tokens && w > cap) return fail(BLT_ERR_SHAPE, "tokenize_bytes: capacity too small");
+  return BLT_OK;
+}
+
+int blt_ingest_plan_chunks(int64_t doc_len, int32_t chunk_len, int32_t overlap,
+                           int64_t* starts, int32_t* lens, int32_t* skips, int64_t cap) {
+  if (doc_len < 0 || chunk_len <= 0 || overlap < 0 || 2 * (int64_t)overlap > chunk_len)
+    return fail(BLT_ERR_SHAPE, "plan_chunks: doc_len >= 0, 0 <= 2 * overlap <= chunk_len");
+  std::vector<ChunkPlan> c;
+  plan_chunks(doc_len, chunk_len, overlap, c);
+  if ((int64_t)c.size() > cap) return fail(BLT_ERR_SHAPE, "plan_chunks: capacity too small");
+  if ((int64_t)c.size() > 0x7fffffff) return fail(BLT_ERR_SHAPE, "plan_chunks: too many chunks");
+  for (size_t i = 0; i < c.size(); ++i) {
+    if (starts) starts[i] = c[i].start;
+    if (lens) lens[i] = c[i].len;
+    if (skips) skips[i] = c[i].skip;
+  }
+  return (int)c.size();
+}
+
+int blt_ingest_create(blt_model* m, const blt_ingest_config* cfg, blt_ingest** out) {
+  if (!m || !cfg || !out) return fail(BLT_ERR_INVALID, "ingest_create: null argument");
+  Ingest* g = new Ingest();
+  const int rc = g->init(reinterpret_cast<Model*>(m), *cfg);
+  if (rc) {
+    delete g;
+    return rc;
+  }
+  *out = reinterpret_cast<blt_ingest*>(g);
+  return BLT_OK;
+}
+
+int blt_ingest_destroy(blt_ingest* g) {
+  delete reinterpret_cast<Ingest*>(g);
+  return BLT_OK;
+}
+
+int blt_ingest_run(blt_ingest* g, const int32_t* tokens, const int64_t* doc_offsets,
+                   int64_t n_docs, float* entropies, float* norms, float* coherence,
+                   float* embeddings, int32_t* starts, int32_t* lengths, int32_t* counts) {
+  if (!g) return fail(BLT_ERR_INVALID, "ingest_run: null handle");
+  if (n_docs < 0) return fail(BLT_ERR_SHAPE, "ingest_run: n_docs >= 0");
+  if (n_docs == 0) return BLT_OK;
+  if (!doc_offsets || (!tokens && doc_offsets[n_docs] > 0))
+    return fail(BLT_ERR_INVALID, "ingest_run: null argument");
+  if (doc_offsets[0] != 0) return fail(BLT_ERR_SHAPE, "ingest_run: doc_offsets[0] must be 0");
+  return reinterpret_cast<Ingest*>(g)->run(tokens, doc_offsets, n_docs, entropies, norms,
+                                           coherence, embeddings, starts, lengths, counts);
+}
+
+}  // extern "C"

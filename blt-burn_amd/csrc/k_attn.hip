@@ -65,18 +65,32 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
   const int qw = q0 + wid * QPW;  // this wave's first query
   const int window = p.causal ? p.window : 0;
 
+  // segment starts (packed rows): clamped to [0, t] so any input stays in range
+  const int32_t* seg = p.seg_start ? p.seg_start + b * T : nullptr;
+  auto seg_at = [&](int t) -> int {
+    if (!seg) return 0;
+    const int tc = t < T - 1 ? t : T - 1;
+    const int v = seg[tc];
+    return v < 0 ? 0 : (v > tc ? tc : v);
+  };
+
   // block key range
   int lo = 0, hi = T - 1;
   if (p.causal) {
     hi = q0 + BQ - 1 < T - 1 ? q0 + BQ - 1 : T - 1;
     if (window > 0) lo = q0 - window + 1 > 0 ? q0 - window + 1 : 0;
+    const int sl = seg_at(q0);  // smallest segment start of the block's queries
+    lo = lo > sl ? lo : sl;
   }
   const int t_begin = lo / BKV, t_end = hi / BKV;
   // wave key range
-  int wlo = 0, whi = T - 1;
+  int wlo = 0, whi = T - 1, wseg_hi = 0;
   if (p.causal) {
     whi = qw + QPW - 1 < T - 1 ? qw + QPW - 1 : T - 1;
     if (window > 0) wlo = qw - window + 1 > 0 ? qw - window + 1 : 0;
+    const int sl = seg_at(qw);
+    wlo = wlo > sl ? wlo : sl;
+    wseg_hi = seg_at(qw + QPW - 1);  // largest segment start of the wave's queries
   }
   const bool wave_active = qw < T;
   const int wt_begin = wlo / BKV, wt_end = whi / BKV;
@@ -176,14 +190,19 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
       // max grows by more than 2^8 (checked wave-wide), so P <= 256 and the
       // O / l rescale is skipped for most tiles; O / l is unchanged by it.
       const bool need_mask = (p.causal && kb + BKV - 1 > qw) ||
-                             (window > 0 && kb <= qw + QPW - 1 - window) || (kb + BKV > T);
+                             (window > 0 && kb <= qw + QPW - 1 - window) || (kb + BKV > T) ||
+                             kb < wseg_hi;
       bf16x8_t pb[NQ][2][2];
 #pragma unroll
       for (int qq = 0; qq < NQ; ++qq) {
         const int qi = qw + 32 * qq + lrow;
         if (need_mask) {
           const int lim_hi = p.causal ? (qi < T - 1 ? qi : T - 1) : T - 1;  // key <= lim_hi
-          const int lim_lo = window > 0 ? qi - window : -1;                  // key > lim_lo
+          int lim_lo = window > 0 ? qi - window : -1;                        // key > lim_lo
+          if (p.causal) {
+            const int sg = seg_at(qi) - 1;
+            lim_lo = lim_lo > sg ? lim_lo : sg;
+          }
 #pragma unroll
           for (int sub = 0; sub < 2; ++sub)
 #pragma unroll

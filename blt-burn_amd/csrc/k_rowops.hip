@@ -6,6 +6,7 @@
 // 8-byte bf16 vector loads, fully coalesced), so each row is read from HBM
 // exactly once and all reductions are wave shuffles.  Rows wider than the
 // register budget fall back to a streaming variant that re-reads the row.
+#include "../../include/blt_hip.h"
 #include "rowops.hpp"
 
 #include <math.h>
@@ -368,18 +369,26 @@ __global__ __launch_bounds__(256) void rope_kernel(const uint16_t* __restrict__ 
 #define PB_THREADS 1024
 #define PB_ITEMS 8
 
+// Row b covers H[off_b, off_b + T_b): off_b = b * T and T_b = T for a dense
+// [B, T] input, or row_off[b] / row_len[b] for variable-length rows (the
+// per-document pass of the ingest driver).  mask / starts / lengths use the
+// same offsets as H.
 __global__ __launch_bounds__(PB_THREADS) void patch_boundary_kernel(
-    const float* __restrict__ H, int64_t T, float thr, int mode, int32_t* __restrict__ mask,
-    int32_t* __restrict__ starts, int32_t* __restrict__ lengths, int32_t* __restrict__ count) {
+    const float* __restrict__ H, int64_t T_dense, float thr, int mode,
+    int32_t* __restrict__ mask, int32_t* __restrict__ starts, int32_t* __restrict__ lengths,
+    int32_t* __restrict__ count, const int64_t* __restrict__ row_off,
+    const int32_t* __restrict__ row_len) {
   __shared__ int wave_tot[PB_THREADS / BLT_WAVE];
   __shared__ int carry_s;
   const int64_t b = blockIdx.x;
-  const float* h = H + b * T;
+  const int64_t roff = row_off ? row_off[b] : b * T_dense;
+  const int64_t T = row_len ? (int64_t)row_len[b] : T_dense;
+  const float* h = H + roff;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   if (tid == 0) carry_s = 0;
   __syncthreads();
-  for (int64_t base = 0; base < T; base += (int64_t)PB_THREADS * PB_ITEMS) {
-    const int64_t p0 = base + (int64_t)tid * PB_ITEMS;
+  for (int64_t t0 = 0; t0 < T; t0 += (int64_t)PB_THREADS * PB_ITEMS) {
+    const int64_t p0 = t0 + (int64_t)tid * PB_ITEMS;
     int flags[PB_ITEMS];
     int local = 0;
     float prev = (p0 >= 1 && p0 - 1 < T) ? h[p0 - 1] : 0.f;
@@ -393,7 +402,7 @@ __global__ __launch_bounds__(PB_THREADS) void patch_boundary_kernel(
         else if (mode == 0) f = (cur - prev) > thr;
         else f = cur > thr;
         prev = cur;
-        if (mask) mask[b * T + t] = f;
+        if (mask) mask[roff + t] = f;
       }
       flags[k] = f;
       local += f;
@@ -423,7 +432,7 @@ __global__ __launch_bounds__(PB_THREADS) void patch_boundary_kernel(
     if (starts) {
 #pragma unroll
       for (int k = 0; k < PB_ITEMS; ++k)
-        if (flags[k]) starts[b * T + pos++] = (int32_t)(p0 + k);
+        if (flags[k]) starts[roff + pos++] = (int32_t)(p0 + k);
     }
     __syncthreads();
     if (tid == PB_THREADS - 1) carry_s = carry + wave_tot[wid] + incl;
@@ -435,9 +444,9 @@ __global__ __launch_bounds__(PB_THREADS) void patch_boundary_kernel(
     __threadfence_block();
     __syncthreads();
     for (int i = tid; i < n; i += PB_THREADS) {
-      const int32_t s = starts[b * T + i];
-      const int32_t e = (i + 1 < n) ? starts[b * T + i + 1] : (int32_t)T;
-      lengths[b * T + i] = e - s;
+      const int32_t s = starts[roff + i];
+      const int32_t e = (i + 1 < n) ? starts[roff + i + 1] : (int32_t)T;
+      lengths[roff + i] = e - s;
     }
   }
 }
@@ -617,7 +626,73 @@ int launch_patch_boundaries(const float* H, int64_t B, int64_t T, float thr, int
                             hipStream_t s) {
   if (B == 0) return 0;
   hipLaunchKernelGGL(patch_boundary_kernel, dim3((unsigned)B), dim3(PB_THREADS), 0, s, H, T, thr,
-                     mode, mask, starts, lengths, count);
+                     mode, mask, starts, lengths, count, nullptr, nullptr);
+  BLT_LAUNCH_CHECK("patch_boundary_kernel");
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// ingest helpers
+// ---------------------------------------------------------------------------
+// Stitch packed-row outputs into per-document order: dest[i] >= 0 sends token
+// i's entropy / norm / coherence there; -1 drops it (overlap context or
+// padding).  C / Co may be null.
+__global__ __launch_bounds__(256) void scatter_tokens_kernel(
+    const int32_t* __restrict__ dest, const float* __restrict__ H, const float* __restrict__ N,
+    const float* __restrict__ C, float* __restrict__ Ho, float* __restrict__ No,
+    float* __restrict__ Co, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int32_t d = dest[i];
+    if (d >= 0) {
+      Ho[d] = H[i];
+      No[d] = N[i];
+      if (C) Co[d] = C[i];
+    }
+  }
+}
+
+// The same stitch for [n, dim] f32 rows (pre-norm embeddings): one wave per
+// row, 16-byte loads and stores (dim % 4 == 0, rows 16-byte aligned).
+__global__ __launch_bounds__(256) void scatter_rows_kernel(const int32_t* __restrict__ dest,
+                                                           const float* __restrict__ X,
+                                                           float* __restrict__ Xo, int64_t n,
+                                                           int dim) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= n) return;
+  const int32_t d = dest[row];
+  if (d < 0) return;
+  const f32x4_t* src = reinterpret_cast<const f32x4_t*>(X + row * dim);
+  f32x4_t* dst = reinterpret_cast<f32x4_t*>(Xo + (int64_t)d * dim);
+  for (int c = threadIdx.x & 63; c < dim / 4; c += 64) dst[c] = src[c];
+}
+
+int launch_scatter_tokens(const int32_t* dest, const float* H, const float* N, const float* C,
+                          float* Ho, float* No, float* Co, int64_t n, hipStream_t s) {
+  if (n == 0) return 0;
+  if ((C == nullptr) != (Co == nullptr)) return fail(BLT_ERR_INVALID, "scatter: C and Co pair");
+  hipLaunchKernelGGL(scatter_tokens_kernel, dim3(elementwise_grid(n)), dim3(256), 0, s, dest, H,
+                     N, C, Ho, No, Co, n);
+  BLT_LAUNCH_CHECK("scatter_tokens_kernel");
+  return 0;
+}
+int launch_scatter_rows(const int32_t* dest, const float* X, float* Xo, int64_t n, int dim,
+                        hipStream_t s) {
+  if (n == 0) return 0;
+  if (dim % 4 || ((uintptr_t)X | (uintptr_t)Xo) % 16)
+    return fail(BLT_ERR_SHAPE, "scatter_rows: dim % 4 == 0 and 16-byte aligned rows");
+  hipLaunchKernelGGL(scatter_rows_kernel, dim3(ceil_div(n, 4)), dim3(256), 0, s, dest, X, Xo, n,
+                     dim);
+  BLT_LAUNCH_CHECK("scatter_rows_kernel");
+  return 0;
+}
+int launch_patch_boundaries_varlen(const float* H, const int64_t* row_off, const int32_t* row_len,
+                                   int64_t rows, float thr, int mode, int32_t* mask,
+                                   int32_t* starts, int32_t* lengths, int32_t* count,
+                                   hipStream_t s) {
+  if (rows == 0) return 0;
+  hipLaunchKernelGGL(patch_boundary_kernel, dim3((unsigned)rows), dim3(PB_THREADS), 0, s, H,
+                     (int64_t)0, thr, mode, mask, starts, lengths, count, row_off, row_len);
   BLT_LAUNCH_CHECK("patch_boundary_kernel");
   return 0;
 }

@@ -225,7 +225,7 @@ int Model::create(int dev, const blt_model_config& c, const blt_model_weights& w
 }
 
 int Model::forward(const int32_t* tokens, int64_t B, int64_t T, const blt_model_outputs& o,
-                   hipStream_t s) {
+                   hipStream_t s, const int32_t* seg_start) {
   if (tokens == nullptr) return fail(-1, "forward: tokens is null");
   if (B < 0 || T < 0) return fail(-2, "forward: negative shape");
   if (T > cfg.max_seqlen) return fail(-2, "forward: seq_len exceeds max_seqlen");
@@ -255,6 +255,7 @@ int Model::forward(const int32_t* tokens, int64_t B, int64_t T, const blt_model_
     g.A = a; g.Bt = wqkv + l * 3 * D * D; g.C = qkv;
     g.M = M; g.N = 3 * D; g.K = D; g.lda = D; g.ldb = D; g.ldc = 3 * D;
     g.epi = EPI_QKV_ROPE; g.rope_cols = (int)(2 * D); g.seq_len = T; g.rope_cs = rope_cs;
+    g.seg_start = seg_start;
     if ((rc = launch_gemm(g, s))) return rc;
     if ((rc = mark(BLT_STAGE_QKV_GEMM, s))) return rc;
     AttnArgs at{};
@@ -264,7 +265,7 @@ int Model::forward(const int32_t* tokens, int64_t B, int64_t T, const blt_model_
     at.sb_k = T * 3 * D; at.sh_k = 64; at.st_k = 3 * D;
     at.sb_v = T * 3 * D; at.sh_v = 64; at.st_v = 3 * D;
     at.sb_o = T * D; at.sh_o = 64; at.st_o = D;
-    at.causal = 1; at.window = cfg.window;
+    at.causal = 1; at.window = cfg.window; at.seg_start = seg_start;
     if ((rc = launch_attention(at, s))) return rc;
     if ((rc = mark(BLT_STAGE_ATTENTION, s))) return rc;
     g = GemmArgs{};

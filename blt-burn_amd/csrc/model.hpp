@@ -49,7 +49,7 @@ struct Model {
   static int create(int dev, const blt_model_config& c, const blt_model_weights& w,
                     int64_t max_tok, Model** out);
   int forward(const int32_t* tokens, int64_t B, int64_t T, const blt_model_outputs& o,
-              hipStream_t s);
+              hipStream_t s, const int32_t* seg_start = nullptr);
 };
 
 }  // namespace blt

@@ -24,6 +24,15 @@ int launch_patch_boundaries(const float* H, int64_t B, int64_t T, float thr, int
                             int32_t* mask, int32_t* starts, int32_t* lengths, int32_t* count,
                             hipStream_t s);
 
+int launch_scatter_tokens(const int32_t* dest, const float* H, const float* N, const float* C,
+                          float* Ho, float* No, float* Co, int64_t n, hipStream_t s);
+int launch_scatter_rows(const int32_t* dest, const float* X, float* Xo, int64_t n, int dim,
+                        hipStream_t s);
+int launch_patch_boundaries_varlen(const float* H, const int64_t* row_off, const int32_t* row_len,
+                                   int64_t rows, float thr, int mode, int32_t* mask,
+                                   int32_t* starts, int32_t* lengths, int32_t* count,
+                                   hipStream_t s);
+
 // k_gemm.hip -----------------------------------------------------------------
 // C[M, N] = A[M, K] . Bt[N, K]^T with bf16 operands and f32 accumulation; the
 // epilogue decides what is written.  K % 64 == 0, N % 64 == 0 (Bt padded with
@@ -44,7 +53,8 @@ struct GemmArgs {
   int epi;
   int n_valid;      // EPI_F32
   int rope_cols;    // EPI_QKV_ROPE
-  int64_t seq_len;  // EPI_QKV_ROPE: position = row % seq_len
+  int64_t seq_len;  // EPI_QKV_ROPE: position = row % seq_len - seg_start[row]
+  const int32_t* seg_start;  // segment starts within each row (NULL = 0)
   const float* rope_cs;  // [max_seqlen, 32, 2]
   int vec_ok;            // EPI_F32: C and ldc allow 16-byte row stores
   int group_m;           // tile order: M-tiles per group (0 = N fastest)
@@ -57,6 +67,10 @@ struct AttnArgs {
   int64_t B, H, T;
   int64_t sb_q, sh_q, st_q, sb_k, sh_k, st_k, sb_v, sh_v, st_v, sb_o, sh_o, st_o;
   int causal, window;
+  // Optional packed segments: seg_start[b * T + t] = index (within the row) of
+  // the first token of t's segment, non-decreasing along a row.  Key j is
+  // visible to query i only if j >= seg_start[i].  NULL = one segment per row.
+  const int32_t* seg_start;
 };
 int launch_attention(const AttnArgs& a, hipStream_t s);
 

@@ -118,11 +118,17 @@ class LMTransformer:
     def device_bytes(self):
         return _lib.lib().blt_model_device_bytes(self._h)
 
-    def forward_with_embeddings(self, tokens, out=None):
+    def forward_with_embeddings(self, tokens, out=None, seg_start=None):
         """tokens: int32 [batch, seq] on this GPU.  Returns ModelOutput with logits
         [B, T, V] f32, pre_norm_embeddings [B, T, D] f32, embedding_norms [B, T],
         entropies [B, T], coherence_scores [B, T].  `out` may hold preallocated
-        tensors under those names (reused, nothing allocated)."""
+        tensors under those names (reused, nothing allocated).
+
+        seg_start (optional int32 [B, T] on this GPU): position of the first
+        token of each token's segment, non-decreasing along a row.  Several
+        independent sequences then share one row: attention stays inside a
+        segment and RoPE positions restart at each segment start, so every
+        segment's outputs equal a separate forward of that segment alone."""
         require_cuda(tokens)
         if tokens.dim() != 2:
             raise BltError("forward_with_embeddings expects tokens [batch, seq]")
@@ -141,8 +147,17 @@ class LMTransformer:
                 raise BltError("output %s must be contiguous f32 %s" % (n, shp))
             res[n] = t
         o = ModelOutputs(*[res[n].data_ptr() for n in _lib.OUTPUT_FIELDS])
-        check(_lib.lib().blt_model_forward(self._h, tok.data_ptr(), B, T, ctypes.byref(o),
-                                           stream_ptr(tok.device)), "blt_model_forward")
+        if seg_start is None:
+            check(_lib.lib().blt_model_forward(self._h, tok.data_ptr(), B, T, ctypes.byref(o),
+                                               stream_ptr(tok.device)), "blt_model_forward")
+        else:
+            require_cuda(seg_start)
+            if tuple(seg_start.shape) != (B, T) or seg_start.dtype != torch.int32 \
+                    or not seg_start.is_contiguous():
+                raise BltError("seg_start must be contiguous int32 [batch, seq]")
+            check(_lib.lib().blt_model_forward_segments(
+                self._h, tok.data_ptr(), seg_start.data_ptr(), B, T, ctypes.byref(o),
+                stream_ptr(tok.device)), "blt_model_forward_segments")
         return ModelOutput(**res)
 
     def set_profiling(self, on=True):

@@ -203,6 +203,17 @@ int64_t blt_model_device_bytes(const blt_model* m);
 int blt_model_forward(blt_model* m, const int32_t* tokens, int64_t B, int64_t T,
                       const blt_model_outputs* out, blt_stream_t stream);
 
+/* Packed rows: several independent sequences (segments) per row, as the
+ * reference would run them one by one (model.rs:269-322 per sequence; the
+ * document loop of batching.rs:5-15 / blt_core.rs:300-356).  seg_start [B, T]
+ * int32 device buffer: for token t of row b, the index within the row of the
+ * first token of t's segment (non-decreasing along the row).  Attention of a
+ * token sees only keys of its own segment, and its RoPE position is
+ * t - seg_start[b, t]; every other op is per token. */
+int blt_model_forward_segments(blt_model* m, const int32_t* tokens, const int32_t* seg_start,
+                               int64_t B, int64_t T, const blt_model_outputs* out,
+                               blt_stream_t stream);
+
 /* Per-stage timing of blt_model_forward with HIP events recorded on the
  * forward's stream between its kernels (for roofline reporting). */
 typedef enum blt_stage {
@@ -225,6 +236,58 @@ int blt_model_set_profiling(blt_model* m, int32_t on);
  * launch counts for the forwards since the previous read (n >= BLT_NUM_STAGES). */
 int blt_model_read_profile(blt_model* m, double* ms, int64_t* launches, int32_t n);
 const char* blt_stage_name(int32_t stage);
+
+/* Byte tokenizer (host) ---------------------------------------------------- */
+
+/* BltTokenizer::encode(String::from_utf8_lossy(bytes)) without BPE
+ * (tokenizer.rs:76-103 on the text built at blt_core.rs:152-154): every
+ * maximal ill-formed UTF-8 subsequence becomes U+FFFD (EF BF BD), each byte b
+ * becomes b + 4, BOS (1) first and EOS (2) last when asked.  tokens may be
+ * null to only count; otherwise at most cap tokens are written and a larger
+ * result is BLT_ERR_SHAPE.  *n_tokens receives the count. */
+int blt_tokenize_bytes(const uint8_t* bytes, int64_t n, int32_t add_bos, int32_t add_eos,
+                       int32_t* tokens, int64_t cap, int64_t* n_tokens);
+
+/* Streaming ingest --------------------------------------------------------- */
+
+/* Replaces the per-document loop of blt_core.rs:145-228 after tokenization
+ * (compute_all_signals_chunked at blt_core.rs:286-370, the monotonic or
+ * global boundary pass, patch indices / lengths, coherence) for many
+ * documents at once.  Chunks of at most chunk_len tokens (the first covers
+ * [0, chunk_len - overlap); later ones start overlap tokens early and drop
+ * their first overlap outputs) are packed into batches of `rows` rows of
+ * `row_len` tokens, each chunk its own attention / RoPE segment; a document
+ * always lies in one batch. */
+typedef struct blt_ingest_config {
+  int32_t rows;            /* packed rows per batch */
+  int32_t row_len;         /* tokens per packed row (<= model max_seqlen) */
+  int32_t chunk_len;       /* BltConfig::max_seq_len; 0 means row_len */
+  int32_t overlap;         /* BltConfig::chunk_overlap; 2 * overlap <= chunk_len */
+  float threshold;         /* BltConfig::threshold */
+  int32_t mode;            /* blt_patch_mode (BltConfig::monotonicity) */
+  int32_t with_embeddings; /* != 0: return pre-norm embeddings as well */
+} blt_ingest_config;
+typedef struct blt_ingest blt_ingest;
+
+/* Host-only: the chunk plan of one document of doc_len tokens (blt_core.rs:
+ * 300-356).  Writes up to cap entries; returns the number of chunks (>= 0)
+ * or a negative blt_status. */
+int blt_ingest_plan_chunks(int64_t doc_len, int32_t chunk_len, int32_t overlap, int64_t* starts,
+                           int32_t* lens, int32_t* skips, int64_t cap);
+/* Allocates two pinned host + device buffer sets, an upload and a download
+ * stream.  The model must have max_tokens >= rows * row_len. */
+int blt_ingest_create(blt_model* m, const blt_ingest_config* cfg, blt_ingest** out);
+int blt_ingest_destroy(blt_ingest* g);
+/* Document d is tokens[doc_offsets[d], doc_offsets[d + 1]) (doc_offsets[0] =
+ * 0, n_docs + 1 entries).  Outputs are host memory indexed like the tokens:
+ * entropies / norms / coherence [total], embeddings [total, dim] (only with
+ * with_embeddings), starts / lengths [total] with document d's patches at
+ * doc_offsets[d] .. + counts[d], counts [n_docs].  Any output may be null.
+ * Starts are positions inside the document (patch_start_indices_cpu).
+ * Returns when every output is written. */
+int blt_ingest_run(blt_ingest* g, const int32_t* tokens, const int64_t* doc_offsets,
+                   int64_t n_docs, float* entropies, float* norms, float* coherence,
+                   float* embeddings, int32_t* starts, int32_t* lengths, int32_t* counts);
 
 /* Synthetic inputs (host memory, deterministic across C and Python) ----- */
 

@@ -212,3 +212,57 @@ def model_forward(cfg, weights, tokens):
                                  ("logits", "pre_norm_embeddings", "embedding_norms",
                                   "entropies", "coherence_scores")])
     return out
+
+
+def chunk_plan(total, chunk, overlap):
+    """compute_all_signals_chunked's loop (blt_core.rs:286-356) as (start, end, skip)
+    triples, stated exactly as the reference states it (saturating subtraction,
+    skip = overlap for every later chunk)."""
+    stride = chunk - overlap
+    out = []
+    pos = 0
+    while pos < total:
+        start = 0 if pos == 0 else max(pos - overlap, 0)
+        end = min(pos + stride, total)
+        skip = 0 if pos == 0 else overlap
+        out.append((start, end, skip))
+        pos = end
+    return out
+
+
+def signals_chunked(cfg, weights, tokens, chunk, overlap):
+    """blt_core.rs:286-370 over one document: one B=1 forward per chunk, the
+    kept outputs appended in order, then truncated / zero-padded to the
+    document length.  Returns (entropies [n], embeddings [n, D], norms [n])."""
+    tokens = np.asarray(tokens, dtype=np.int32)
+    n = tokens.size
+    D = cfg["dim"]
+    H, E, N = [], [], []
+    for start, end, skip in chunk_plan(n, chunk, overlap):
+        o = model_forward(cfg, weights, tokens[None, start:end])
+        for i in range(skip, end - start):
+            if len(H) < n:
+                H.append(o["entropies"][0, i])
+                N.append(o["embedding_norms"][0, i])
+                E.append(o["pre_norm_embeddings"][0, i])
+    while len(H) < n:
+        H.append(np.float32(0))
+        N.append(np.float32(0))
+        E.append(np.zeros(D, np.float32))
+    return (np.array(H, np.float32), np.array(E, np.float32).reshape(n, D),
+            np.array(N, np.float32))
+
+
+def process_document(cfg, weights, tokens, chunk, overlap, threshold, mode=0):
+    """process_bytes_with_embeddings after tokenization (blt_core.rs:178-207):
+    dict(entropies, norms, embeddings, coherence, starts, lengths)."""
+    H, E, N = signals_chunked(cfg, weights, tokens, chunk, overlap)
+    if H.size == 0:
+        z = np.zeros(0, np.int32)
+        return dict(entropies=H, norms=N, embeddings=E, coherence=H.copy(), starts=z, lengths=z)
+    m = patch_mask(H[None, :], threshold, mode)
+    s = patch_indices(m)
+    ln = patch_lengths(s, H.size)
+    coh = (N * N) / (H + np.float32(1e-6))
+    return dict(entropies=H, norms=N, embeddings=E, coherence=coh.astype(np.float32),
+                starts=np.array(s[0], np.int32), lengths=np.array(ln[0], np.int32))

@@ -1,0 +1,213 @@
+"""Streaming ingest on the GPU: packed-segment forwards and the native ingest
+driver (blt_ingest_run) against the CPU oracle's restatement of
+compute_all_signals_chunked + the boundary pass (blt_core.rs:178-207,
+286-370), and against separate GPU forwards of each chunk.
+
+Tolerances: entropies 2e-2 abs and norms 1e-2 rel against the oracle (the
+stated bound); against separate GPU forwards of the same chunks the only
+difference is the attention kernel's key-tile alignment (online-softmax
+order), so 5e-3 abs / rel there.  Boundaries, patch lengths and coherence are
+bit-exact given the same entropies / norms."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from blt_burn_amd import BltError
+from blt_burn_amd import ingest as I
+from blt_burn_amd import model as M
+from blt_burn_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(dim=128, n_layers=2, n_heads=2, ffn_dim_multiplier=2.0, multiple_of=64,
+            max_seqlen=512, vocab_size=260)
+
+
+def _oracle_cfg(cfg, hidden, window):
+    return dict(dim=cfg.dim, n_layers=cfg.n_layers, n_heads=cfg.resolved_n_heads(),
+                hidden=hidden, vocab=cfg.vocab_size, max_seqlen=cfg.max_seqlen,
+                norm_eps=cfg.norm_eps, rope_theta=cfg.rope_theta, window=window)
+
+
+def _oracle_weights(w):
+    f = {k: synth.bf16_to_f32(v) for k, v in w.items()}
+    return {"emb": f["tok_embeddings"], "attn_norm": f["attention_norm"],
+            "ffn_norm": f["ffn_norm"], "wq": f["wq"], "wk": f["wk"], "wv": f["wv"],
+            "wo": f["wo"], "w1": f["w1"], "w2": f["w2"], "w3": f["w3"], "norm": f["norm"],
+            "out": f["output"]}
+
+
+def _seg_start(rows_lens, T):
+    seg = np.zeros((len(rows_lens), T), np.int32)
+    for b, lens in enumerate(rows_lens):
+        assert sum(lens) == T
+        p = 0
+        for n in lens:
+            seg[b, p:p + n] = p
+            p += n
+    return seg
+
+
+def _check_segments(m, tok, rows_lens, tol):
+    B, T = tok.shape
+    seg = _seg_start(rows_lens, T)
+    packed = m.forward_with_embeddings(torch.from_numpy(tok).cuda(),
+                                       seg_start=torch.from_numpy(seg).cuda())
+    H = packed.entropies.cpu().numpy()
+    N = packed.embedding_norms.cpu().numpy()
+    worst = [0.0, 0.0]
+    for b, lens in enumerate(rows_lens):
+        p = 0
+        for n in lens:
+            one = m.forward_with_embeddings(torch.from_numpy(tok[b:b + 1, p:p + n].copy()).cuda())
+            h1 = one.entropies.cpu().numpy()[0]
+            n1 = one.embedding_norms.cpu().numpy()[0]
+            worst[0] = max(worst[0], np.abs(H[b, p:p + n] - h1).max())
+            worst[1] = max(worst[1], (np.abs(N[b, p:p + n] - n1) / n1).max())
+            p += n
+    print("segments vs separate: entropy max|d|=%.2e norms max rel=%.2e" % tuple(worst))
+    assert worst[0] < tol and worst[1] < tol, worst
+
+
+@pytest.mark.parametrize("window", [0, 24])
+def test_segments_match_separate_forwards_tiny(window):
+    cfg = M.LMTransformerConfig(**TINY)
+    w = M.random_weights(cfg, 21, hidden=256)
+    m = M.LMTransformer(cfg, w, device=0, max_tokens=2 * 256, window=window)
+    tok = synth.tokens(synth.config_seed(5) + 1, (2, 256))
+    _check_segments(m, tok, [[40, 100, 1, 115], [256]], 5e-3)
+
+
+@pytest.mark.parametrize("window,B", [(512, 1), (0, 3)])
+def test_segments_match_separate_forwards_entropy_model(window, B):
+    # real dims and T = 8192; window 0 with B = 3 takes the 64-query-wave
+    # attention path, window 512 the 32-query one
+    cfg = M.entropy_model_config()
+    cfg.n_layers = 2
+    w = M.random_weights(cfg, 22, hidden=2048)
+    m = M.LMTransformer(cfg, w, device=0, max_tokens=B * 8192, window=window)
+    tok = synth.tokens(synth.config_seed(5) + 2, (B, 8192))
+    rows = [[3000, 64, 63, 5065], [8192], [1, 4095, 4096]][:B]
+    _check_segments(m, tok, rows, 5e-3)
+
+
+def _docs(seed, lens):
+    toks = synth.tokens(seed, (max(1, sum(lens)),))[: sum(lens)]
+    off = np.zeros(len(lens) + 1, np.int64)
+    off[1:] = np.cumsum(lens)
+    return toks.astype(np.int32), off
+
+
+def _check_doc_outputs(res, d, ref_H, ref_N, tolH, tolN, thr, mode):
+    H, N, C, S, Ln = res.doc(d)[:5]
+    assert H.size == ref_H.size
+    if H.size == 0:
+        assert res.counts[d] == 0
+        return 0.0, 0.0
+    dH = np.abs(H - ref_H).max()
+    dN = (np.abs(N - ref_N) / np.maximum(ref_N, 1e-30)).max()
+    assert dH < tolH and dN < tolN, (d, dH, dN)
+    # coherence exactly as blt_core.rs:202-207 on these norms / entropies
+    np.testing.assert_array_equal(C, (N * N) / (H + np.float32(1e-6)))
+    # boundaries bit-exact on the same entropies (patcher.rs:80-164)
+    m = oracle.patch_mask(H[None, :], thr, mode)
+    s = oracle.patch_indices(m)
+    np.testing.assert_array_equal(S, np.array(s[0], np.int32))
+    np.testing.assert_array_equal(Ln, np.array(oracle.patch_lengths(s, H.size)[0], np.int32))
+    assert int(Ln.sum()) == H.size
+    return dH, dN
+
+
+@pytest.mark.parametrize("window", [0, 24])
+def test_ingest_vs_oracle_tiny(window):
+    cfg = M.LMTransformerConfig(**TINY)
+    w = M.random_weights(cfg, 23, hidden=256)
+    m = M.LMTransformer(cfg, w, device=0, max_tokens=4 * 128, window=window)
+    conf = I.BltConfig(threshold=0.35, max_seq_len=64, chunk_overlap=16)
+    ing = I.StreamingIngest(m, conf, rows=4, row_len=128, with_embeddings=True)
+    lens = [0, 1, 2, 37, 64, 65, 150, 300, 5, 0, 128, 49]
+    toks, off = _docs(synth.config_seed(5) + 3, lens)
+    res = ing.run(toks, off)
+    oc, ow = _oracle_cfg(cfg, 256, window), _oracle_weights(w)
+    worst = [0.0, 0.0]
+    for d in range(len(lens)):
+        ref = oracle.process_document(oc, ow, toks[off[d]:off[d + 1]], 64, 16, 0.35)
+        dH, dN = _check_doc_outputs(res, d, ref["entropies"], ref["norms"], 2e-2, 1e-2, 0.35, 0)
+        worst = [max(worst[0], dH), max(worst[1], dN)]
+        if lens[d]:
+            E = res.embeddings[off[d]:off[d + 1]]
+            rel = np.abs(E - ref["embeddings"]).max() / np.abs(ref["embeddings"]).max()
+            assert rel < 1e-2, (d, rel)
+    print("ingest vs oracle: entropy max|d|=%.2e norms max rel=%.2e" % tuple(worst))
+    assert res.counts[0] == 0 and res.counts[9] == 0
+
+
+def _direct_chunks(m, toks, chunk, overlap):
+    """The reference loop with the GPU model: one forward per chunk."""
+    H = np.zeros(toks.size, np.float32)
+    N = np.zeros(toks.size, np.float32)
+    for s, n, k in I.plan_chunks(toks.size, chunk, overlap):
+        o = m.forward_with_embeddings(torch.from_numpy(toks[None, s:s + n].copy()).cuda())
+        H[s + k:s + n] = o.entropies.cpu().numpy()[0, k:]
+        N[s + k:s + n] = o.embedding_norms.cpu().numpy()[0, k:]
+    return H, N
+
+
+def test_ingest_config5_sample_entropy_model():
+    # config-5 shape at real dims: 8192-token rows, 512 overlap, log-normal
+    # documents (a 160 KiB sample of the 1 GiB stream), full 14 layers
+    cfg = M.entropy_model_config()
+    w = M.random_weights(cfg, 24, hidden=2048)
+    # a 16384-token document is chunks of 7680, 8192 and 1536 tokens: 3 rows
+    m = M.LMTransformer(cfg, w, device=0, max_tokens=3 * 8192, window=512)
+    conf = I.BltConfig(threshold=1.335, max_seq_len=8192, chunk_overlap=512)
+    ing = I.StreamingIngest(m, conf, rows=3, row_len=8192)
+    data, off = synth.documents(synth.config_seed(5), 160 * 1024, max_len=16384)
+    toks = data.astype(np.int32) + 4
+    res = ing.run(toks, off)
+    worst = [0.0, 0.0]
+    for d in range(off.size - 1):
+        H, N = _direct_chunks(m, toks[off[d]:off[d + 1]], 8192, 512)
+        dH, dN = _check_doc_outputs(res, d, H, N, 5e-3, 5e-3, 1.335, 0)
+        worst = [max(worst[0], dH), max(worst[1], dN)]
+    print("ingest vs per-chunk forwards (%d docs): entropy max|d|=%.2e norms max rel=%.2e"
+          % (off.size - 1, worst[0], worst[1]))
+
+
+def test_process_bytes_mirror():
+    cfg = M.LMTransformerConfig(**TINY)
+    w = M.random_weights(cfg, 25, hidden=256)
+    m = M.LMTransformer(cfg, w, device=0, max_tokens=512, window=0)
+    conf = I.BltConfig(max_seq_len=64, chunk_overlap=16, add_bos=True, add_eos=True)
+    data = "héllo, wörld \xff".encode("latin-1", errors="replace") + b"\xf0\x90 tail" * 9
+    ex = I.process_bytes_with_embeddings(data, "doc-1", m, conf)
+    toks = ex.core.tokens
+    assert toks[0] == 1 and toks[-1] == 2
+    assert ex.core.sample_id == "doc-1" and ex.core.mask.all() and ex.core.mask.size == toks.size
+    assert ex.pre_norm_embeddings.size == toks.size * cfg.dim and ex.embedding_dim == cfg.dim
+    assert int(ex.core.patch_lengths.sum()) == toks.size
+    ref = oracle.process_document(_oracle_cfg(cfg, 256, 0), _oracle_weights(w), toks, 64, 16,
+                                  1.335)
+    assert np.abs(ex.core.entropies - ref["entropies"]).max() < 2e-2
+    core = I.process_bytes(data, "doc-1", m, conf)
+    np.testing.assert_array_equal(core.tokens, toks)
+    assert np.abs(core.entropies - ex.core.entropies).max() < 1e-6
+    empty = I.process_bytes(b"", "e", m, I.BltConfig(max_seq_len=64, chunk_overlap=16))
+    assert empty.tokens.size == 0 and empty.patch_lengths.size == 0
+
+
+def test_ingest_rejects_bad_shapes():
+    cfg = M.LMTransformerConfig(**TINY)
+    w = M.random_weights(cfg, 26, hidden=256)
+    m = M.LMTransformer(cfg, w, device=0, max_tokens=256, window=0)
+    with pytest.raises(BltError):
+        I.StreamingIngest(m, I.BltConfig(max_seq_len=64, chunk_overlap=40), rows=2, row_len=128)
+    with pytest.raises(BltError):  # rows * row_len above the model's max_tokens
+        I.StreamingIngest(m, I.BltConfig(max_seq_len=64, chunk_overlap=16), rows=4, row_len=128)
+    ing = I.StreamingIngest(m, I.BltConfig(max_seq_len=64, chunk_overlap=16), rows=2, row_len=64)
+    toks, off = _docs(7, [10, 400])  # 400 tokens need 8 chunks of 64: more than 2 rows
+    with pytest.raises(BltError):
+        ing.run(toks, off)
+    res = ing.run(*_docs(8, [10, 20]))  # the handle still works after the error
+    assert res.counts.size == 2 and int(res.lengths[:res.counts[0]].sum()) == 10
