@@ -48,9 +48,11 @@ EXPORTS = {
     "blt_model_forward": (c_i32, [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp]),
     "blt_model_forward_segments": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp]),
     "blt_tokenize_bytes": (c_i32, [c_vp, c_i64, c_i32, c_i32, c_vp, c_i64, c_vp]),
+    "blt_tokenize_documents": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_i64, c_vp]),
     "blt_ingest_plan_chunks": (c_i32, [c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i64]),
     "blt_ingest_create": (c_i32, [c_vp, c_vp, c_vp]),
     "blt_ingest_destroy": (c_i32, [c_vp]),
+    "blt_ingest_last_stats": (c_i32, [c_vp, c_vp]),
     "blt_ingest_run": (c_i32, [c_vp, c_vp, c_vp, c_i64] + [c_vp] * 7),
     "blt_model_set_profiling": (c_i32, [c_vp, c_i32]),
     "blt_model_read_profile": (c_i32, [c_vp, ctypes.POINTER(c_f64), ctypes.POINTER(c_i64), c_i32]),
@@ -88,6 +90,12 @@ OUTPUT_FIELDS = ("logits", "pre_norm_embeddings", "embedding_norms", "entropies"
 
 class ModelOutputs(ctypes.Structure):
     _fields_ = [(n, c_vp) for n in OUTPUT_FIELDS]
+
+
+class IngestStats(ctypes.Structure):
+    """blt_ingest_stats."""
+    _fields_ = [("batches", c_i64), ("documents", c_i64), ("tokens", c_i64),
+                ("tokens_computed", c_i64), ("row_tokens", c_i64)]
 
 
 class IngestConfig(ctypes.Structure):

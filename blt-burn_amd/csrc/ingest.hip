@@ -73,11 +73,17 @@ static bool pack_chunks(const std::vector<ChunkPlan>& c, std::vector<int64_t>& f
   return true;
 }
 
+// Documents examined per batch after the oldest pending one; later ones that
+// fit the space left are packed too (outputs go to each document's own
+// offsets, so the order of batches does not matter).
+static constexpr size_t kLookahead = 1024;
+
 struct Ingest {
   Model* m = nullptr;
   blt_ingest_config cfg{};
   int64_t BT = 0, dim = 0;
   hipStream_t up = nullptr, ks = nullptr, down = nullptr;
+  blt_ingest_stats stats{};
 
   struct Slot {
     // pinned host
@@ -230,24 +236,40 @@ int Ingest::run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, f
                                      std::to_string(L) + " tokens does not fit one batch");
   }
   BLT_HIP_CHECK(hipSetDevice(m->device));
+  stats = blt_ingest_stats{};
+  // documents still to run, in input order; empty ones have no outputs
+  // (blt_core.rs:160-176) and never enter a batch
+  std::vector<int64_t> pending;
+  pending.reserve((size_t)n_docs);
+  for (int64_t d = 0; d < n_docs; ++d)
+    if (doc_off[d + 1] > doc_off[d]) pending.push_back(d);
+  std::vector<char> taken(pending.size(), 0);
+  size_t head = 0;
   int k = 0, rc;
-  int64_t d = 0;
-  while (d < n_docs) {
+  while (head < pending.size()) {
     Slot& s = slot[k];
     if ((rc = finish(s, doc_off, ent, nrm, coh, emb, starts, lens, counts))) return rc;
     std::fill(fill.begin(), fill.end(), 0);
     s.docs.clear();
     s.out_tokens = 0;
-    // ---- pack whole documents until the next one does not fit ----
-    for (; d < n_docs; ++d) {
+    // ---- pack whole documents: the oldest pending one first (it always fits
+    // an empty batch), then any of the next kLookahead that still fit ----
+    int64_t free_tokens = BT;
+    size_t scanned = 0;
+    for (size_t i = head; i < pending.size() && scanned < kLookahead && free_tokens > 0; ++i) {
+      if (taken[i]) continue;
+      ++scanned;
+      const int64_t d = pending[i];
       const int64_t L = doc_off[d + 1] - doc_off[d];
-      if (L == 0) continue;  // empty documents have no outputs (blt_core.rs:160-176)
+      if (L > free_tokens) continue;
       plan_chunks(L, cfg.chunk_len, cfg.overlap, chunks);
-      if (!pack_chunks(chunks, fill, T, order, row, col)) break;
+      if (!pack_chunks(chunks, fill, T, order, row, col)) continue;
+      taken[i] = 1;
       const int64_t jd = (int64_t)s.docs.size();
       s.h_doff[jd] = s.out_tokens;
       s.h_dlen[jd] = (int32_t)L;
       const int32_t* src = tokens + doc_off[d];
+      int64_t computed = 0;
       for (size_t ci = 0; ci < chunks.size(); ++ci) {
         const ChunkPlan& c = chunks[ci];
         const int64_t base = row[ci] * T + col[ci];
@@ -257,11 +279,16 @@ int Ingest::run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, f
           s.h_seg[base + j] = (int32_t)col[ci];
           s.h_dest[base + j] = j < c.skip ? -1 : out0 + j;
         }
+        computed += c.len;
       }
+      free_tokens -= computed;
       s.out_tokens += L;
       s.docs.push_back(d);
+      stats.documents += 1;
+      stats.tokens += L;
+      stats.tokens_computed += computed;
     }
-    if (s.docs.empty()) break;  // only empty documents were left
+    while (head < pending.size() && taken[head]) ++head;
     // padding: every free position is its own one-token segment, output dropped
     for (int64_t r = 0; r < B; ++r)
       for (int64_t c = fill[r]; c < T; ++c) {
@@ -270,6 +297,8 @@ int Ingest::run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, f
         s.h_dest[r * T + c] = -1;
       }
     const int64_t nd = (int64_t)s.docs.size();
+    stats.batches += 1;
+    stats.row_tokens += BT;
     // ---- upload ----
     BLT_HIP_CHECK(hipMemcpyAsync(s.d_tok, s.h_tok, (size_t)BT * 4, hipMemcpyHostToDevice, up));
     BLT_HIP_CHECK(hipMemcpyAsync(s.d_seg, s.h_seg, (size_t)BT * 4, hipMemcpyHostToDevice, up));
@@ -391,6 +420,26 @@ int blt_tokenize_bytes(const uint8_t* bytes, int64_t n, int32_t add_bos, int32_t
   return BLT_OK;
 }
 
+int blt_tokenize_documents(const uint8_t* bytes, const int64_t* byte_offsets, int64_t n_docs,
+                           int32_t add_bos, int32_t add_eos, int32_t* tokens, int64_t cap,
+                           int64_t* token_offsets) {
+  if (n_docs < 0 || !byte_offsets || !token_offsets)
+    return fail(BLT_ERR_INVALID, "tokenize_documents: bad argument");
+  if (byte_offsets[0] != 0) return fail(BLT_ERR_SHAPE, "tokenize_documents: offsets[0] != 0");
+  token_offsets[0] = 0;
+  for (int64_t d = 0; d < n_docs; ++d) {
+    const int64_t n = byte_offsets[d + 1] - byte_offsets[d];
+    if (n < 0) return fail(BLT_ERR_SHAPE, "tokenize_documents: offsets must be non-decreasing");
+    const int64_t w = token_offsets[d];
+    int64_t got = 0;
+    const int rc = blt_tokenize_bytes(bytes + byte_offsets[d], n, add_bos, add_eos,
+                                      tokens ? tokens + w : nullptr, tokens ? cap - w : 0, &got);
+    if (rc) return rc;
+    token_offsets[d + 1] = w + got;
+  }
+  return BLT_OK;
+}
+
 int blt_ingest_plan_chunks(int64_t doc_len, int32_t chunk_len, int32_t overlap,
                            int64_t* starts, int32_t* lens, int32_t* skips, int64_t cap) {
   if (doc_len < 0 || chunk_len <= 0 || overlap < 0 || 2 * (int64_t)overlap > chunk_len)
@@ -416,6 +465,12 @@ int blt_ingest_create(blt_model* m, const blt_ingest_config* cfg, blt_ingest** o
     return rc;
   }
   *out = reinterpret_cast<blt_ingest*>(g);
+  return BLT_OK;
+}
+
+int blt_ingest_last_stats(blt_ingest* g, blt_ingest_stats* out) {
+  if (!g || !out) return fail(BLT_ERR_INVALID, "ingest_last_stats: null argument");
+  *out = reinterpret_cast<Ingest*>(g)->stats;
   return BLT_OK;
 }
 

@@ -72,28 +72,36 @@ int Model::mark(int stage, hipStream_t s) {
   return 0;
 }
 
-// Sum the time between consecutive marks per stage (stage -1 = the start
-// mark of a forward), then forget the marks.
-int Model::read_profile(double* ms, int64_t* launches, int n) {
-  for (int i = 0; i < n; ++i) {
-    ms[i] = 0.0;
-    launches[i] = 0;
-  }
-  if (!ev_marks.empty()) BLT_HIP_CHECK(hipEventSynchronize(ev_pool[ev_marks.back().second]));
+// Add the time between consecutive marks to the per-stage totals (stage -1 =
+// the start mark of a forward), then recycle the events.
+int Model::fold_profile() {
+  if (ev_marks.empty()) return 0;
+  BLT_HIP_CHECK(hipEventSynchronize(ev_pool[ev_marks.back().second]));
   for (size_t i = 1; i < ev_marks.size(); ++i) {
     const int st = ev_marks[i].first;
-    if (st < 0) continue;
+    if (st < 0 || st >= BLT_NUM_STAGES) continue;
     float t = 0.f;
     BLT_HIP_CHECK(hipEventElapsedTime(&t, ev_pool[ev_marks[i - 1].second],
                                       ev_pool[ev_marks[i].second]));
-    if (st < n) {
-      ms[st] += t;
-      launches[st] += 1;
-    }
+    acc_ms[st] += t;
+    acc_n[st] += 1;
   }
   ev_marks.clear();
   ev_used = 0;
   return 0;
+}
+
+int Model::read_profile(double* ms, int64_t* launches, int n) {
+  const int rc = fold_profile();
+  for (int i = 0; i < n; ++i) {
+    ms[i] = i < BLT_NUM_STAGES ? acc_ms[i] : 0.0;
+    launches[i] = i < BLT_NUM_STAGES ? acc_n[i] : 0;
+  }
+  for (int i = 0; i < BLT_NUM_STAGES; ++i) {
+    acc_ms[i] = 0.0;
+    acc_n[i] = 0;
+  }
+  return rc;
 }
 
 Model::~Model() {
@@ -239,9 +247,8 @@ int Model::forward(const int32_t* tokens, int64_t B, int64_t T, const blt_model_
   float* xr = o.pre_norm_embeddings ? o.pre_norm_embeddings : x;
   int rc;
   if (profiling && ev_used + 16 * (cfg.n_layers + 1) > 4096) {
-    // unread marks pile up: keep the pool bounded by dropping them
-    ev_marks.clear();
-    ev_used = 0;
+    // keep the event pool bounded: wait for the marks so far and sum them
+    if ((rc = fold_profile())) return rc;
   }
   if ((rc = mark(-1, s))) return rc;
   if ((rc = launch_embed(tokens, emb, xr, M, (int)D, (int)V, s))) return rc;

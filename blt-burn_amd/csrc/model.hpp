@@ -43,6 +43,9 @@ struct Model {
   std::vector<std::pair<int, size_t>> ev_marks;  // (stage, index of the event ending it)
   hipStream_t ev_stream = nullptr;
   int mark(int stage, hipStream_t s);  // records the event that ends `stage`
+  double acc_ms[BLT_NUM_STAGES] = {};  // totals of folded marks
+  int64_t acc_n[BLT_NUM_STAGES] = {};
+  int fold_profile();
   int read_profile(double* ms, int64_t* launches, int n);
 
   ~Model();

@@ -15,7 +15,7 @@ from typing import Optional
 import numpy as np
 
 from . import _lib
-from ._lib import PATCH_GLOBAL, PATCH_MONOTONIC, BltError, IngestConfig, check
+from ._lib import PATCH_GLOBAL, PATCH_MONOTONIC, BltError, IngestConfig, IngestStats, check
 from .tokenizer import OFFSET, tokenize_bytes
 
 
@@ -114,7 +114,8 @@ class StreamingIngest:
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h is not None and h.value and _lib._lib is not None:
+        # at interpreter exit the module globals may already be gone
+        if h is not None and h.value and _lib is not None and _lib._lib is not None:
             _lib.lib().blt_ingest_destroy(h)
             self._h = None
 
@@ -138,6 +139,13 @@ class StreamingIngest:
             p(res.coherence), p(res.embeddings), p(res.starts), p(res.lengths), p(res.counts)),
             "blt_ingest_run")
         return res
+
+    def last_stats(self):
+        """Counts of the last run(): dict(batches, documents, tokens, tokens_computed,
+        row_tokens)."""
+        st = IngestStats()
+        check(_lib.lib().blt_ingest_last_stats(self._h, ctypes.byref(st)), "ingest_last_stats")
+        return {n: int(getattr(st, n)) for n, _ in IngestStats._fields_}
 
     def process(self, docs, sample_ids=None):
         """bytes documents -> [BltExampleWithEmbeddings] (process_bytes_with_embeddings

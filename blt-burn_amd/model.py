@@ -111,7 +111,8 @@ class LMTransformer:
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h is not None and h.value and _lib._lib is not None:
+        # at interpreter exit the module globals may already be gone
+        if h is not None and h.value and _lib is not None and _lib._lib is not None:
             _lib.lib().blt_model_destroy(h)
             self._h = None
 

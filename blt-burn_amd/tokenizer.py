@@ -34,6 +34,24 @@ def tokenize_bytes(data, add_bos=False, add_eos=False):
     return out[: n.value].copy()
 
 
+def tokenize_documents(data, byte_offsets, add_bos=False, add_eos=False):
+    """Concatenated documents data[byte_offsets[d]:byte_offsets[d + 1]] ->
+    (tokens int32 [total], token_offsets int64 [n_docs + 1]); each document is
+    tokenized on its own, as tokenize_bytes."""
+    buf = np.ascontiguousarray(np.frombuffer(data, dtype=np.uint8) if isinstance(
+        data, (bytes, bytearray)) else data, dtype=np.uint8)
+    boff = np.ascontiguousarray(byte_offsets, dtype=np.int64)
+    nd = boff.size - 1
+    cap = 3 * buf.size + 2 * nd
+    out = np.empty(max(cap, 1), dtype=np.int32)
+    toff = np.zeros(nd + 1, dtype=np.int64)
+    check(_lib.lib().blt_tokenize_documents(buf.ctypes.data if buf.size else None,
+                                            boff.ctypes.data, nd, int(add_bos), int(add_eos),
+                                            out.ctypes.data, cap, toff.ctypes.data),
+          "blt_tokenize_documents")
+    return out[: toff[-1]].copy(), toff
+
+
 class BltTokenizer:
     """BltTokenizer::new(add_bos, add_eos) without BPE delimiters (tokenizer.rs:12-36)."""
 

@@ -248,6 +248,15 @@ const char* blt_stage_name(int32_t stage);
 int blt_tokenize_bytes(const uint8_t* bytes, int64_t n, int32_t add_bos, int32_t add_eos,
                        int32_t* tokens, int64_t cap, int64_t* n_tokens);
 
+/* The same over n_docs documents bytes[byte_offsets[d], byte_offsets[d + 1])
+ * (byte_offsets[0] = 0): document d's tokens go to tokens[token_offsets[d],
+ * token_offsets[d + 1]) (token_offsets has n_docs + 1 entries, [0] = 0).
+ * 3 * bytes + 2 * n_docs tokens always suffice; tokens may be null to only
+ * count. */
+int blt_tokenize_documents(const uint8_t* bytes, const int64_t* byte_offsets, int64_t n_docs,
+                           int32_t add_bos, int32_t add_eos, int32_t* tokens, int64_t cap,
+                           int64_t* token_offsets);
+
 /* Streaming ingest --------------------------------------------------------- */
 
 /* Replaces the per-document loop of blt_core.rs:145-228 after tokenization
@@ -288,6 +297,17 @@ int blt_ingest_destroy(blt_ingest* g);
 int blt_ingest_run(blt_ingest* g, const int32_t* tokens, const int64_t* doc_offsets,
                    int64_t n_docs, float* entropies, float* norms, float* coherence,
                    float* embeddings, int32_t* starts, int32_t* lengths, int32_t* counts);
+/* Counts of the last blt_ingest_run: non-empty documents and their tokens,
+ * tokens run through the model (chunks, overlap context included) and
+ * packed-row slots launched (batches * rows * row_len, padding included). */
+typedef struct blt_ingest_stats {
+  int64_t batches;
+  int64_t documents;
+  int64_t tokens;
+  int64_t tokens_computed;
+  int64_t row_tokens;
+} blt_ingest_stats;
+int blt_ingest_last_stats(blt_ingest* g, blt_ingest_stats* out);
 
 /* Synthetic inputs (host memory, deterministic across C and Python) ----- */
 

@@ -166,6 +166,12 @@ def test_ingest_config5_sample_entropy_model():
     data, off = synth.documents(synth.config_seed(5), 160 * 1024, max_len=16384)
     toks = data.astype(np.int32) + 4
     res = ing.run(toks, off)
+    st = ing.last_stats()
+    lens = np.diff(off)
+    assert st["documents"] == int((lens > 0).sum()) and st["tokens"] == int(lens.sum())
+    assert st["tokens_computed"] == sum(n for L in lens for _, n, _ in I.plan_chunks(int(L), 8192,
+                                                                                       512))
+    assert st["row_tokens"] == st["batches"] * 3 * 8192 >= st["tokens_computed"]
     worst = [0.0, 0.0]
     for d in range(off.size - 1):
         H, N = _direct_chunks(m, toks[off[d]:off[d + 1]], 8192, 512)

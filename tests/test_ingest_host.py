@@ -107,3 +107,17 @@ def test_plan_chunks_rejects_large_overlap():
         I.plan_chunks(100, 1024, 513)
     with pytest.raises(BltError):
         I.plan_chunks(100, 0, 0)
+
+
+def test_tokenize_documents_matches_per_document():
+    data, off = synth.documents(synth.config_seed(5), 200_000)
+    toks, toff = tk.tokenize_documents(data, off, add_bos=True, add_eos=False)
+    assert toff.size == off.size and toff[0] == 0
+    raw = data.tobytes()
+    for d in range(off.size - 1):
+        one = tk.tokenize_bytes(raw[off[d]:off[d + 1]], add_bos=True)
+        np.testing.assert_array_equal(toks[toff[d]:toff[d + 1]], one)
+    # a truncated sequence at a document's end does not join the next document
+    t2, o2 = tk.tokenize_documents(b"\xe2\x82\xac", np.array([0, 2, 3]))
+    assert t2.tolist() == [0xEF + 4, 0xBF + 4, 0xBD + 4, 0xEF + 4, 0xBF + 4, 0xBD + 4]
+    assert o2.tolist() == [0, 3, 6]
