@@ -51,7 +51,7 @@ def _dispatch_stages(names, layers):
     """Map the kernel names of one forward's dispatches, in order, to model stages."""
     out, g = [], 0
     for n in names:
-        if "gemm_bf16_kernel" in n:
+        if "gemm_bf16" in n:
             out.append(STAGE_OF_GEMM[g % 4] if g < 4 * layers else "head_gemm")
             g += 1
         elif "attn_fwd_kernel" in n:
@@ -160,7 +160,19 @@ def main():
     ap.add_argument("--copy-bytes", type=float, default=float(2 ** 30))
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                     help="print per-stage kernel durations from rocprofv3 --kernel-trace output")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="run one device copy of --copy-bytes bytes (the counter calibration "
+                         "kernel for --summarize) and exit")
     args = ap.parse_args()
+    if args.copy_probe:
+        import torch
+        x = torch.ones(int(args.copy_bytes) // 4, device="cuda")
+        y = torch.empty_like(x)
+        torch.cuda.synchronize()
+        y.copy_(x)
+        torch.cuda.synchronize()
+        print("copied %d bytes" % (x.numel() * 4))
+        return
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
         return
