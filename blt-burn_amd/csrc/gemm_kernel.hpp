@@ -73,11 +73,86 @@ __device__ inline int64_t rope_pos(const GemmArgs& p, int64_t row) {
   return t - s;
 }
 
+// The factor of each of this lane's accumulator rows (row0 + 32 i); 1 when
+// the GEMM does not carry a norm.
+template <class C>
+__device__ inline void load_row_scales(const GemmArgs& p, int64_t row0, float (&rs)[C::TM]) {
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i) {
+    const int64_t r = row0 + i * 32;
+    rs[i] = p.row_scale ? p.row_scale[r < p.M ? r : p.M - 1] : 1.f;
+  }
+}
+
+template <class C>
+__device__ inline void scale_rows(f32x16_t (&acc)[C::TM][C::TN], const float (&rs)[C::TM]) {
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] *= rs[i];
+}
+
+// Sum over each aligned group of 16 lanes, result in every lane of the group:
+// DPP quad permutes (xor 1, xor 2), then mirrors within 8 and within 16 lanes.
+template <int CTRL>
+__device__ inline float dpp_f32(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ inline float sum16(float v) {
+  v += dpp_f32<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_f32<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_f32<0x141>(v);  // row_half_mirror
+  v += dpp_f32<0x140>(v);  // row_mirror
+  return v;
+}
+
 template <class C>
 __device__ inline void epilogue(const GemmArgs& p, f32x16_t (&acc)[C::TM][C::TN], int64_t m0,
-                                int64_t n0, int wm, int wn, int lrow, int lhalf) {
+                                int64_t n0, int wm, int wn, int lrow, int lhalf,
+                                const float (&rs)[C::TM]) {
   const int64_t row_base = m0 + wm * C::WTM + lrow;
   const int64_t col_base = n0 + wn * C::WTN + 4 * lhalf;
+  if (p.row_scale) scale_rows<C>(acc, rs);
+  if (p.epi == EPI_RESID_F32) {
+    // N % 64 == 0, ldc % 4 == 0.  Lanes l and l + 32 share a row and hold its
+    // 64 columns of this wave tile between them.
+    static_assert(C::WTN == 64, "norm partial sums are per 64 columns");
+    const int64_t wcol = n0 + wn * C::WTN;
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) {
+      const int64_t row = row_base + i * 32;
+      const bool rok = row < p.M;
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int64_t col = col_base + j * 32 + 8 * g;
+          if (!rok || col >= p.N) continue;
+          f32x4_t* o =
+              reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(p.C) + row * p.ldc + col);
+          f32x4_t x = *o;
+          x.x += acc[i][j][4 * g];
+          x.y += acc[i][j][4 * g + 1];
+          x.z += acc[i][j][4 * g + 2];
+          x.w += acc[i][j][4 * g + 3];
+          *o = x;
+          if (p.xb_out) {
+            *reinterpret_cast<u32x2_t*>(p.xb_out + row * p.ldc + col) =
+                u32x2_t{pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w)};
+            ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+          }
+        }
+      if (p.ss_out) {
+        ss += __shfl_xor(ss, 32, 64);
+        if (lhalf == 0 && rok && wcol < p.N) p.ss_out[row * p.ss_np + wcol / 64] = ss;
+      }
+    }
+    return;
+  }
   if (p.epi == EPI_QKV_ROPE || p.epi == EPI_SILU_GATE) {
     // pairs: sub-tile 2j holds columns c, sub-tile 2j+1 holds c + 32 of the same 64-group
     uint16_t* out = reinterpret_cast<uint16_t*>(p.C);
@@ -155,7 +230,7 @@ __device__ inline void epilogue(const GemmArgs& p, f32x16_t (&acc)[C::TM][C::TN]
           w.x = pack_bf16x2(v[0], v[1]);
           w.y = pack_bf16x2(v[2], v[3]);
           *reinterpret_cast<u32x2_t*>(reinterpret_cast<uint16_t*>(p.C) + row * p.ldc + col) = w;
-        } else if (p.epi == EPI_F32) {
+        } else {  // EPI_F32
           float* o = reinterpret_cast<float*>(p.C) + row * p.ldc + col;
           if (col + 3 < p.n_valid && p.vec_ok) {
             *reinterpret_cast<f32x4_t*>(o) = f32x4_t{v[0], v[1], v[2], v[3]};
@@ -164,15 +239,6 @@ __device__ inline void epilogue(const GemmArgs& p, f32x16_t (&acc)[C::TM][C::TN]
             for (int e = 0; e < 4; ++e)
               if (col + e < p.n_valid) o[e] = v[e];
           }
-        } else {  // EPI_RESID_F32: N % 64 == 0, ldc % 4 == 0
-          if (col >= p.N) continue;
-          f32x4_t* o = reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(p.C) + row * p.ldc + col);
-          f32x4_t x = *o;
-          x.x += v[0];
-          x.y += v[1];
-          x.z += v[2];
-          x.w += v[3];
-          *o = x;
         }
       }
   }
@@ -285,8 +351,11 @@ void gemm_bf16_kernel(GemmArgs p) {
   };
 
   const int KT = (int)(p.K / BK);
-  // prologue: tile 0 -> LDS stage 0, tiles 1 .. PF in flight in their sets
+  // prologue: tile 0 -> LDS stage 0, tiles 1 .. PF in flight in their sets;
+  // the row factors are fetched under tile 0's load latency
   gload(ra[0], rb[0], 0);
+  float rs[C::TM];
+  load_row_scales<C>(p, m0 + wm * C::WTM + lrow, rs);
   sstore(ra[0], rb[0], 0);
 #pragma unroll
   for (int t = 1; t <= PF; ++t)
@@ -306,7 +375,7 @@ void gemm_bf16_kernel(GemmArgs p) {
     });
   }
 
-  epilogue<C>(p, acc, m0, n0, wm, wn, lrow, lhalf);
+  epilogue<C>(p, acc, m0, n0, wm, wn, lrow, lhalf, rs);
 }
 
 // ---- LDS-staged epilogue for the DMA kernel.  After the main loop each wave
@@ -325,10 +394,11 @@ __device__ inline void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::
 template <class C>
 __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C::TN], int64_t m0,
                                     int64_t n0, int wid, int wm, int wn, int lane,
-                                    unsigned char* smem) {
+                                    unsigned char* smem, const float (&rs)[C::TM]) {
   const int lrow = lane & 31, lhalf = lane >> 5;
   const int64_t row0 = m0 + wm * C::WTM;  // first row of this wave's tile
   const int64_t col0 = n0 + wn * C::WTN;  // first column (pre-epilogue index)
+  if (p.row_scale) scale_rows<C>(acc, rs);
   if (p.epi == EPI_RESID_F32 || p.epi == EPI_F32) {
     constexpr int LD = C::WTN + 2;  // f32 row pitch (8-byte pad)
     float* buf = reinterpret_cast<float*>(smem) + wid * 32 * LD;
@@ -351,18 +421,32 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
         const int64_t col = col0 + c * 4;
         const float* sp = buf + r * LD + c * 4;
         f32x4_t v = f32x4_t{sp[0], sp[1], sp[2], sp[3]};
-        if (row >= p.M || col >= p.N) continue;
-        float* o = reinterpret_cast<float*>(p.C) + row * p.ldc + col;
-        if (p.epi == EPI_RESID_F32) {
-          const f32x4_t x = *reinterpret_cast<const f32x4_t*>(o);
-          v += x;
-          *reinterpret_cast<f32x4_t*>(o) = v;
-        } else if (col + 3 < p.n_valid && p.vec_ok) {
-          *reinterpret_cast<f32x4_t*>(o) = v;
-        } else {
+        const bool ok = row < p.M && col < p.N;
+        float ss = 0.f;
+        if (ok) {
+          float* o = reinterpret_cast<float*>(p.C) + row * p.ldc + col;
+          if (p.epi == EPI_RESID_F32) {
+            const f32x4_t x = *reinterpret_cast<const f32x4_t*>(o);
+            v += x;
+            *reinterpret_cast<f32x4_t*>(o) = v;
+            if (p.xb_out) {
+              *reinterpret_cast<u32x2_t*>(p.xb_out + row * p.ldc + col) =
+                  u32x2_t{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
+              ss = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+          } else if (col + 3 < p.n_valid && p.vec_ok) {
+            *reinterpret_cast<f32x4_t*>(o) = v;
+          } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (col + e < p.n_valid) o[e] = v[e];
+            for (int e = 0; e < 4; ++e)
+              if (col + e < p.n_valid) o[e] = v[e];
+          }
+        }
+        if (p.ss_out) {
+          // CPR == 16: lanes 16k .. 16k + 15 hold the 64 columns of one row
+          static_assert(C::WTN == 64, "norm partial sums are per 64 columns");
+          ss = sum16(ss);
+          if (c == 0 && ok) p.ss_out[row * p.ss_np + col0 / 64] = ss;
         }
       }
       wave_lds_fence();
@@ -543,25 +627,36 @@ void gemm_bf16_dma_kernel(GemmArgs p) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int lrow = lane & 31, lhalf = lane >> 5;
-  auto compute = [&](int stage) {
+  auto load_frags = [&](int stage, int ks, bf16x8_t (&af)[C::TM], bf16x8_t (&bfr)[C::TN]) {
     const uint16_t* sa = lds + stage * C::STAGE;
     const uint16_t* sb = sa + BM * BK;
+    const int chunk = ks * 2 + lhalf;
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int chunk = ks * 2 + lhalf;
-      bf16x8_t af[C::TM], bfr[C::TN];
+    for (int i = 0; i < C::TM; ++i)
+      af[i] = *reinterpret_cast<const bf16x8_t*>(sa + swz<BK>(wm * C::WTM + i * 32 + lrow, chunk));
 #pragma unroll
-      for (int i = 0; i < C::TM; ++i)
-        af[i] = *reinterpret_cast<const bf16x8_t*>(sa + swz<BK>(wm * C::WTM + i * 32 + lrow, chunk));
-#pragma unroll
-      for (int j = 0; j < C::TN; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8_t*>(sb + swz<BK>(wn * C::WTN + j * 32 + lrow, chunk));
+    for (int j = 0; j < C::TN; ++j)
+      bfr[j] = *reinterpret_cast<const bf16x8_t*>(sb + swz<BK>(wn * C::WTN + j * 32 + lrow, chunk));
+  };
+  // Fragments are double-buffered: the LDS reads of K step ks + 1 are issued
+  // before the MFMAs of step ks, and scheduling barriers keep the compiler
+  // from sinking them back next to their uses, so each wave has LDS reads in
+  // flight while its MFMAs run.
+  auto compute = [&](int stage) {
+    bf16x8_t af[2][C::TM], bfr[2][C::TN];
+    load_frags(stage, 0, af[0], bfr[0]);
+    static_for<0, BK / 16>([&](auto kc) {
+      constexpr int ks = decltype(kc)::value;
+      if constexpr (ks + 1 < BK / 16) load_frags(stage, ks + 1, af[(ks + 1) & 1], bfr[(ks + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < C::TM; ++i)
 #pragma unroll
         for (int j = 0; j < C::TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
-    }
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks & 1][j], af[ks & 1][i],
+                                                              acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    });
   };
 
   // Wait until tile kt's chunks have landed, allowing the `after` tiles issued
@@ -574,6 +669,9 @@ void gemm_bf16_dma_kernel(GemmArgs p) {
   const int KT = (int)(p.K / BK);
   const int pre = KT < S - 1 ? KT : S - 1;  // tiles issued in the prologue
   for (int t = 0; t < pre; ++t) dma_tile(t, t);
+  // row factors, fetched under the prologue tiles' latency
+  float rs[C::TM];
+  load_row_scales<C>(p, m0 + wm * C::WTM + lrow, rs);
   wait_tile(pre - 1);
   int st = 0;  // stage of tile kt
   for (int kt = 0; kt < KT; ++kt) {
@@ -591,7 +689,7 @@ void gemm_bf16_dma_kernel(GemmArgs p) {
 
   // every wave is past its last LDS read of the K loop before LDS is reused
   __syncthreads();
-  epilogue_lds<C>(p, acc, m0, n0, wid, wm, wn, lane, reinterpret_cast<unsigned char*>(lds));
+  epilogue_lds<C>(p, acc, m0, n0, wid, wm, wn, lane, reinterpret_cast<unsigned char*>(lds), rs);
 }
 
 }  // namespace gemm

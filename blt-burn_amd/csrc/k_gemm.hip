@@ -32,6 +32,10 @@ int launch_gemm(const GemmArgs& a_in, hipStream_t s) {
        a.epi == EPI_SILU_GATE) && (a.N % 64 != 0 || a.ldc % 4 != 0 || (uintptr_t)a.C % 16 != 0))
     return fail(-2, "gemm: vector epilogues need N % 64 == 0, ldc % 4 == 0, 16-byte aligned C");
   if (a.K % 64 != 0) return fail(-2, "gemm: K must be a multiple of 64");
+  if ((a.xb_out != nullptr) != (a.ss_out != nullptr) ||
+      (a.xb_out && (a.epi != EPI_RESID_F32 || a.ss_np * 64 != a.N || (uintptr_t)a.xb_out % 8)))
+    return fail(-2, "gemm: norm partials need EPI_RESID_F32, xb_out and ss_out, ss_np = N / 64");
+
   if ((uintptr_t)a.A % 16 != 0 || (uintptr_t)a.Bt % 16 != 0 || a.lda % 8 != 0 || a.ldb % 8 != 0)
     return fail(-2, "gemm: A and Bt rows must be 16-byte aligned (lda, ldb % 8 == 0)");
   // Wide N (QKV, W1|W3): walk groups of 8 M-tiles so the blocks resident on

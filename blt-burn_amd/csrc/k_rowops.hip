@@ -313,10 +313,15 @@ __global__ __launch_bounds__(256) void coherence_kernel(const float* __restrict_
 // token embedding gather: x[r, :] = f32(W[clamp(tok[r]), :])   (nn::Embedding)
 // one wave per token row, 8-byte bf16 loads, 16-byte f32 stores.
 // ---------------------------------------------------------------------------
+// With xb / ss (dim % 64 == 0) the row is also copied as bf16 to xb and its
+// per-64-column sums of squares go to ss [rows, dim / 64]: the inputs of the
+// first layer's QKV GEMM, which applies the RMSNorm itself.
 __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ tok,
                                                     const uint16_t* __restrict__ table,
                                                     float* __restrict__ x, int64_t rows,
-                                                    int dim, int vocab) {
+                                                    int dim, int vocab,
+                                                    uint16_t* __restrict__ xb,
+                                                    float* __restrict__ ss) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -328,6 +333,15 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ 
     float v[4];
     ld4(src, e, v);
     st4(dst, e, v);
+    if (xb) {
+      // the 16 lanes of each 16-lane group hold one 64-column group
+      *reinterpret_cast<u32x2_t*>(xb + row * dim + e) =
+          *reinterpret_cast<const u32x2_t*>(src + e);
+      float q = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+#pragma unroll
+      for (int m = 8; m >= 1; m >>= 1) q += __shfl_xor(q, m, BLT_WAVE);
+      if ((lane & 15) == 0) ss[row * (dim / 64) + e / 64] = q;
+    }
   }
 }
 
@@ -604,11 +618,33 @@ int launch_coherence(const float* nrm, const float* ent, float* out, int64_t n, 
   BLT_LAUNCH_CHECK("coherence_kernel");
   return 0;
 }
-int launch_embed(const int32_t* tok, const uint16_t* table, float* x, int64_t rows, int dim,
-                 int vocab, hipStream_t s) {
+__global__ __launch_bounds__(256) void row_rstd_kernel(const float* __restrict__ ss,
+                                                       float* __restrict__ rstd, int64_t rows,
+                                                       int np, int dim, float eps) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float* s = ss + r * np;
+  float t = 0.f;
+  for (int q = 0; q < np; ++q) t += s[q];
+  rstd[r] = 1.f / (sqrtf(t / (float)dim) + eps);
+}
+
+int launch_row_rstd(const float* ss, float* rstd, int64_t rows, int np, int dim, float eps,
+                    hipStream_t s) {
   if (rows == 0) return 0;
+  hipLaunchKernelGGL(row_rstd_kernel, dim3(ceil_div(rows, 256)), dim3(256), 0, s, ss, rstd, rows,
+                     np, dim, eps);
+  BLT_LAUNCH_CHECK("row_rstd_kernel");
+  return 0;
+}
+
+int launch_embed(const int32_t* tok, const uint16_t* table, float* x, int64_t rows, int dim,
+                 int vocab, hipStream_t s, uint16_t* xb, float* ss) {
+  if (rows == 0) return 0;
+  if ((xb != nullptr) != (ss != nullptr) || (xb && dim % 64))
+    return fail(BLT_ERR_SHAPE, "embed: xb and ss together, dim % 64 == 0");
   hipLaunchKernelGGL(embed_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, s, tok, table, x, rows,
-                     dim, vocab);
+                     dim, vocab, xb, ss);
   BLT_LAUNCH_CHECK("embed_kernel");
   return 0;
 }

@@ -9,13 +9,23 @@
 //                       land in one lane of the GEMM epilogue)
 //     w2   [L, D, F]    w2^T
 //     wout [V, D]       output^T
-//   norm weights as f32; the RoPE cos/sin table [max_seqlen, 32, 2] f32.
-//   workspace for max_tokens rows: residual x f32 [M, D], normed bf16 [M, D],
-//   qkv bf16 [M, 3D] (q, k already rotated), attention out bf16 [M, D],
-//   FFN hidden bf16 [M, F], logits f32 [M, V], entropies/norms f32 [M].
+//   wqkv and w13 carry their layer's RMSNorm weight folded in along K
+//   (W'[n, k] = bf16(W[n, k] * w_norm[k])); the final norm weight as f32; the
+//   RoPE cos/sin table [max_seqlen, 32, 2] f32.
+//   workspace for max_tokens rows: residual x f32 [M, D], bf16 copy of the
+//   residual (or of the final normed rows) [M, D], per-64-column sums of
+//   squares of the residual f32 [M, D / 64] and the row factors 1 / (rms +
+//   eps) f32 [M] made from them, qkv bf16 [M, 3D] (q, k already
+//   rotated), attention out bf16 [M, D], FFN hidden bf16 [M, F], logits f32
+//   [M, V], entropies/norms f32 [M].
 //
-// Per layer: rmsnorm -> QKV GEMM (+RoPE) -> attention -> O GEMM (+= residual)
-//            -> rmsnorm -> W1|W3 GEMM (+SiLU*gate) -> W2 GEMM (+= residual).
+// Per layer: QKV GEMM (RMSNorm scale + RoPE) -> attention -> O GEMM (+=
+// residual, bf16 copy + sums of squares) -> W1|W3 GEMM (RMSNorm scale +
+// SiLU*gate) -> W2 GEMM (+= residual, bf16 copy + sums of squares).  The
+// RMSNorm before each projection (model.rs:508-522, 758-770) is thereby split
+// between the GEMM that produces the residual and the GEMM that consumes it:
+// RMSNorm(x) W = (x * w) W / (rms(x) + eps), the per-row factor applied to
+// the consumer's accumulators.
 #include "model.hpp"
 
 #include <math.h>
@@ -106,8 +116,8 @@ int Model::read_profile(double* ms, int64_t* launches, int n) {
 
 Model::~Model() {
   for (hipEvent_t e : ev_pool) (void)hipEventDestroy(e);
-  void* ptrs[] = {emb, attn_norm, ffn_norm, final_norm, wqkv, wo, w13, w2, wout, rope_cs,
-                  x, a, qkv, attn, hbuf, logits, ent, norms};
+  void* ptrs[] = {emb, final_norm, wqkv, wo,   w13,  w2,     wout, rope_cs, x,
+                  a,   ss,         rstd, qkv,  attn, hbuf,   logits, ent,  norms};
   int prev = -1;
   (void)hipGetDevice(&prev);
   (void)hipSetDevice(device);
@@ -147,8 +157,6 @@ int Model::create(int dev, const blt_model_config& c, const blt_model_weights& w
   int64_t& tb = m->bytes;
   int rc = 0;
   rc |= dalloc(&m->emb, V * D, &tb);
-  rc |= dalloc(&m->attn_norm, L * D, &tb);
-  rc |= dalloc(&m->ffn_norm, L * D, &tb);
   rc |= dalloc(&m->final_norm, D, &tb);
   rc |= dalloc(&m->wqkv, L * 3 * D * D, &tb);
   rc |= dalloc(&m->wo, L * D * D, &tb);
@@ -158,6 +166,8 @@ int Model::create(int dev, const blt_model_config& c, const blt_model_weights& w
   rc |= dalloc(&m->rope_cs, (int64_t)c.max_seqlen * 64, &tb);
   rc |= dalloc(&m->x, max_tok * D, &tb);
   rc |= dalloc(&m->a, max_tok * D, &tb);
+  rc |= dalloc(&m->ss, max_tok * (D / 64), &tb);
+  rc |= dalloc(&m->rstd, max_tok, &tb);
   rc |= dalloc(&m->qkv, max_tok * 3 * D, &tb);
   rc |= dalloc(&m->attn, max_tok * D, &tb);
   rc |= dalloc(&m->hbuf, max_tok * F, &tb);
@@ -192,11 +202,17 @@ int Model::create(int dev, const blt_model_config& c, const blt_model_weights& w
     transpose_into(t.data(), w.output, D, V);
     if ((rc = up(m->wout, t.data(), V * D * 2))) { delete m; return rc; }
   }
+  // fold a norm weight into Bt rows: Bt[n][k] *= w[k], rounded to bf16
+  auto fold = [](uint16_t* bt, int64_t rows, int64_t K, const std::vector<float>& wn,
+                 int64_t off) {
+    for (int64_t n = 0; n < rows; ++n)
+      for (int64_t k = 0; k < K; ++k)
+        bt[n * K + k] = f32_to_bf16(bf16_to_f32(bt[n * K + k]) * wn[off + k]);
+  };
+  std::vector<float> attn_w, ffn_w;
   if (L > 0) {
-    std::vector<float> f = to_f32(w.attention_norm, L * D);
-    if ((rc = up(m->attn_norm, f.data(), L * D * 4))) { delete m; return rc; }
-    f = to_f32(w.ffn_norm, L * D);
-    if ((rc = up(m->ffn_norm, f.data(), L * D * 4))) { delete m; return rc; }
+    attn_w = to_f32(w.attention_norm, L * D);
+    ffn_w = to_f32(w.ffn_norm, L * D);
   }
   std::vector<uint16_t> tmp;
   for (int64_t l = 0; l < L; ++l) {
@@ -204,6 +220,7 @@ int Model::create(int dev, const blt_model_config& c, const blt_model_weights& w
     transpose_into(tmp.data(), w.wq + l * D * D, D, D);
     transpose_into(tmp.data() + D * D, w.wk + l * D * D, D, D);
     transpose_into(tmp.data() + 2 * D * D, w.wv + l * D * D, D, D);
+    fold(tmp.data(), 3 * D, D, attn_w, l * D);
     if ((rc = up(m->wqkv + l * 3 * D * D, tmp.data(), 3 * D * D * 2))) { delete m; return rc; }
     tmp.assign(D * D, 0);
     transpose_into(tmp.data(), w.wo + l * D * D, D, D);
@@ -218,6 +235,7 @@ int Model::create(int dev, const blt_model_config& c, const blt_model_weights& w
       const int64_t col = 32 * g + (cc & 31);
       for (int64_t k = 0; k < D; ++k) tmp[n * D + k] = src[k * F + col];
     }
+    fold(tmp.data(), 2 * F, D, ffn_w, l * D);
     if ((rc = up(m->w13 + l * 2 * F * D, tmp.data(), 2 * F * D * 2))) { delete m; return rc; }
     tmp.assign(D * F, 0);
     transpose_into(tmp.data(), w.w2 + l * F * D, F, D);
@@ -251,18 +269,21 @@ int Model::forward(const int32_t* tokens, int64_t B, int64_t T, const blt_model_
     if ((rc = fold_profile())) return rc;
   }
   if ((rc = mark(-1, s))) return rc;
-  if ((rc = launch_embed(tokens, emb, xr, M, (int)D, (int)V, s))) return rc;
+  // layer 0 reads the embedding rows as bf16 plus their sums of squares
+  const bool carry = cfg.n_layers > 0;
+  if ((rc = launch_embed(tokens, emb, xr, M, (int)D, (int)V, s, carry ? a : nullptr,
+                         carry ? ss : nullptr)))
+    return rc;
+  const int np = (int)(D / 64);
+  if (carry && (rc = launch_row_rstd(ss, rstd, M, np, (int)D, cfg.norm_eps, s))) return rc;
   if ((rc = mark(BLT_STAGE_EMBED, s))) return rc;
   for (int64_t l = 0; l < cfg.n_layers; ++l) {
-    if ((rc = launch_rmsnorm<float, float, uint16_t>(xr, attn_norm + l * D, a, nullptr, M, (int)D,
-                                                     cfg.norm_eps, 0, s)))
-      return rc;
-    if ((rc = mark(BLT_STAGE_RMSNORM, s))) return rc;
     GemmArgs g{};
     g.A = a; g.Bt = wqkv + l * 3 * D * D; g.C = qkv;
     g.M = M; g.N = 3 * D; g.K = D; g.lda = D; g.ldb = D; g.ldc = 3 * D;
     g.epi = EPI_QKV_ROPE; g.rope_cols = (int)(2 * D); g.seq_len = T; g.rope_cs = rope_cs;
     g.seg_start = seg_start;
+    g.row_scale = rstd;
     if ((rc = launch_gemm(g, s))) return rc;
     if ((rc = mark(BLT_STAGE_QKV_GEMM, s))) return rc;
     AttnArgs at{};
@@ -278,21 +299,25 @@ int Model::forward(const int32_t* tokens, int64_t B, int64_t T, const blt_model_
     g = GemmArgs{};
     g.A = attn; g.Bt = wo + l * D * D; g.C = xr;
     g.M = M; g.N = D; g.K = D; g.lda = D; g.ldb = D; g.ldc = D; g.epi = EPI_RESID_F32;
+    g.xb_out = a; g.ss_out = ss; g.ss_np = np;
     if ((rc = launch_gemm(g, s))) return rc;
+    if ((rc = launch_row_rstd(ss, rstd, M, np, (int)D, cfg.norm_eps, s))) return rc;
     if ((rc = mark(BLT_STAGE_O_GEMM, s))) return rc;
-    if ((rc = launch_rmsnorm<float, float, uint16_t>(xr, ffn_norm + l * D, a, nullptr, M, (int)D,
-                                                     cfg.norm_eps, 0, s)))
-      return rc;
-    if ((rc = mark(BLT_STAGE_RMSNORM, s))) return rc;
     g = GemmArgs{};
     g.A = a; g.Bt = w13 + l * 2 * F * D; g.C = hbuf;
     g.M = M; g.N = 2 * F; g.K = D; g.lda = D; g.ldb = D; g.ldc = F; g.epi = EPI_SILU_GATE;
+    g.row_scale = rstd;
     if ((rc = launch_gemm(g, s))) return rc;
     if ((rc = mark(BLT_STAGE_W13_GEMM, s))) return rc;
     g = GemmArgs{};
     g.A = hbuf; g.Bt = w2 + l * D * F; g.C = xr;
     g.M = M; g.N = D; g.K = F; g.lda = F; g.ldb = F; g.ldc = D; g.epi = EPI_RESID_F32;
+    const bool next = l + 1 < cfg.n_layers;  // the next layer's QKV GEMM input
+    if (next) {
+      g.xb_out = a; g.ss_out = ss; g.ss_np = np;
+    }
     if ((rc = launch_gemm(g, s))) return rc;
+    if (next && (rc = launch_row_rstd(ss, rstd, M, np, (int)D, cfg.norm_eps, s))) return rc;
     if ((rc = mark(BLT_STAGE_W2_GEMM, s))) return rc;
   }
   // pre-norm L2 norms fused with the final RMSNorm (one read of the residual)

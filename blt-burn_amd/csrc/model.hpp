@@ -17,8 +17,6 @@ struct Model {
   int64_t bytes = 0;
   // packed weights
   uint16_t* emb = nullptr;
-  float* attn_norm = nullptr;
-  float* ffn_norm = nullptr;
   float* final_norm = nullptr;
   uint16_t* wqkv = nullptr;
   uint16_t* wo = nullptr;
@@ -29,6 +27,8 @@ struct Model {
   // workspace
   float* x = nullptr;
   uint16_t* a = nullptr;
+  float* ss = nullptr;
+  float* rstd = nullptr;
   uint16_t* qkv = nullptr;
   uint16_t* attn = nullptr;
   uint16_t* hbuf = nullptr;

@@ -16,8 +16,14 @@ int launch_silu_gate_bf16(const uint16_t* g, const uint16_t* u, uint16_t* o, int
                           hipStream_t s);
 int launch_coherence(const float* nrm, const float* ent, float* out, int64_t n, float eps,
                      hipStream_t s);
+// x = f32 rows of the table; xb (optional) = the same rows in bf16 and ss
+// (optional) = their per-64-column sums of squares [rows, dim / 64]
+// rstd[r] = 1 / (sqrt(sum(ss[r, 0 .. np)) / dim) + eps): the model's RMSNorm
+// factor (eps after the root) from per-64-column sums of squares
+int launch_row_rstd(const float* ss, float* rstd, int64_t rows, int np, int dim, float eps,
+                    hipStream_t s);
 int launch_embed(const int32_t* tok, const uint16_t* table, float* x, int64_t rows, int dim,
-                 int vocab, hipStream_t s);
+                 int vocab, hipStream_t s, uint16_t* xb = nullptr, float* ss = nullptr);
 int launch_rope(const uint16_t* src, uint16_t* dst, const float* cs, int64_t B, int64_t H,
                 int64_t T, int d, int64_t sb, int64_t sh, int64_t st, hipStream_t s);
 int launch_patch_boundaries(const float* H, int64_t B, int64_t T, float thr, int mode,
@@ -58,6 +64,17 @@ struct GemmArgs {
   const float* rope_cs;  // [max_seqlen, 32, 2]
   int vec_ok;            // EPI_F32: C and ldc allow 16-byte row stores
   int group_m;           // tile order: M-tiles per group (0 = N fastest)
+  // RMSNorm carried across GEMMs (model layers).  Producer: an EPI_RESID_F32
+  // GEMM with xb_out set also writes bf16(new residual) to xb_out [M, ldc]
+  // and, per row and 64-column group, the sum of squares of the new residual
+  // to ss_out [M, ss_np] (launch_row_rstd turns those into row factors).
+  // Consumer: a GEMM with row_scale set (its A is such a bf16 residual, its Bt
+  // holds the norm weight folded in) multiplies output row r by row_scale[r]
+  // before its epilogue.
+  uint16_t* xb_out;
+  float* ss_out;
+  int ss_np;
+  const float* row_scale;
 };
 int launch_gemm(const GemmArgs& a, hipStream_t s);
 
