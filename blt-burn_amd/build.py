@@ -21,6 +21,10 @@ FLAGS = [
     "-mcode-object-version=5",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-ffp-contract=fast", "-Wall", "-Wno-unused-function",
+    # keep MFMA sources and results in arch VGPRs: the attention softmax works
+    # on the score accumulators with VALU ops, and results parked in AGPRs cost
+    # a v_accvgpr read/write per value per tile
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", os.path.join(HERE, "..", "include"),
 ]
 

@@ -203,12 +203,14 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
             const int sg = seg_at(qi) - 1;
             lim_lo = lim_lo > sg ? lim_lo : sg;
           }
+          // element (sub, r) holds key kb + 4 * lhalf + (a compile-time offset)
+          const int hi_rel = lim_hi - kb - 4 * lhalf, lo_rel = lim_lo - kb - 4 * lhalf;
 #pragma unroll
           for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              const int key = kb + sub * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-              const bool vis = (key <= lim_hi) & (key > lim_lo);
+              const int ko = sub * 32 + 8 * (r >> 2) + (r & 3);
+              const bool vis = (ko <= hi_rel) & (ko > lo_rel);
               s[qq][sub][r] = vis ? s[qq][sub][r] : -INFINITY;
             }
         }
