@@ -391,18 +391,37 @@ void gemm_bf16_kernel(GemmArgs p) {
 // waits for the wave's outstanding LDS operations.
 __device__ inline void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-template <class C>
+template <class C, int EPI>
 __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C::TN], int64_t m0,
                                     int64_t n0, int wid, int wm, int wn, int lane,
                                     unsigned char* smem, const float (&rs)[C::TM]) {
   const int lrow = lane & 31, lhalf = lane >> 5;
   const int64_t row0 = m0 + wm * C::WTM;  // first row of this wave's tile
   const int64_t col0 = n0 + wn * C::WTN;  // first column (pre-epilogue index)
-  if (p.row_scale) scale_rows<C>(acc, rs);
-  if (p.epi == EPI_RESID_F32 || p.epi == EPI_F32) {
+  // the row factor (1 without a carried norm) is applied as each value is
+  // staged, so the accumulators leave their registers one slab at a time
+  if constexpr (EPI == EPI_RESID_F32 || EPI == EPI_F32) {
     constexpr int LD = C::WTN + 2;  // f32 row pitch (8-byte pad)
     float* buf = reinterpret_cast<float*>(smem) + wid * 32 * LD;
-    constexpr int CPR = C::WTN / 4;  // 16-byte pieces per row
+    constexpr int CPR = C::WTN / 4;       // 16-byte pieces per row
+    constexpr int NP = 32 * CPR / 64;     // pieces per lane per 32-row slab
+    constexpr bool resid = EPI == EPI_RESID_F32;
+    float* Cf = reinterpret_cast<float*>(p.C);
+    // Residual pieces: slab i + 1's are loaded as soon as slab i's have been
+    // added, so their latency overlaps slab i's stores and slab i + 1's
+    // staging (one buffer: the 8-wave kernels have no registers for two).
+    f32x4_t res[NP];
+    auto load_resid = [&](int i) {
+#pragma unroll
+      for (int t = 0; t < NP; ++t) {
+        const int q = lane + 64 * t, r = q / CPR, c = q % CPR;
+        int64_t row = row0 + i * 32 + r, col = col0 + c * 4;
+        row = row < p.M ? row : p.M - 1;  // out-of-range pieces are not stored
+        col = col < p.N ? col : p.N - 4;
+        res[t] = *reinterpret_cast<const f32x4_t*>(Cf + row * p.ldc + col);
+      }
+    };
+    if (resid) load_resid(0);
 #pragma unroll
     for (int i = 0; i < C::TM; ++i) {
 #pragma unroll
@@ -411,69 +430,92 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
         for (int g = 0; g < 4; ++g) {
           float* d = buf + lrow * LD + j * 32 + 8 * g + 4 * lhalf;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) d[e] = acc[i][j][4 * g + e];
+          for (int e = 0; e < 4; ++e) d[e] = acc[i][j][4 * g + e] * rs[i];
         }
       wave_lds_fence();
+      f32x4_t v[NP];
 #pragma unroll
-      for (int t = 0; t < 32 * CPR / 64; ++t) {
+      for (int t = 0; t < NP; ++t) {
+        const int q = lane + 64 * t, r = q / CPR, c = q % CPR;
+        const float* sp = buf + r * LD + c * 4;
+        v[t] = f32x4_t{sp[0], sp[1], sp[2], sp[3]};
+        if (resid) v[t] += res[t];
+      }
+      if (resid && i + 1 < C::TM) load_resid(i + 1);
+#pragma unroll
+      for (int t = 0; t < NP; ++t) {
         const int q = lane + 64 * t, r = q / CPR, c = q % CPR;
         const int64_t row = row0 + i * 32 + r;
         const int64_t col = col0 + c * 4;
-        const float* sp = buf + r * LD + c * 4;
-        f32x4_t v = f32x4_t{sp[0], sp[1], sp[2], sp[3]};
         const bool ok = row < p.M && col < p.N;
         float ss = 0.f;
         if (ok) {
-          float* o = reinterpret_cast<float*>(p.C) + row * p.ldc + col;
-          if (p.epi == EPI_RESID_F32) {
-            const f32x4_t x = *reinterpret_cast<const f32x4_t*>(o);
-            v += x;
-            *reinterpret_cast<f32x4_t*>(o) = v;
+          float* o = Cf + row * p.ldc + col;
+          if (resid) {
+            *reinterpret_cast<f32x4_t*>(o) = v[t];
             if (p.xb_out) {
               *reinterpret_cast<u32x2_t*>(p.xb_out + row * p.ldc + col) =
-                  u32x2_t{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
-              ss = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                  u32x2_t{pack_bf16x2(v[t].x, v[t].y), pack_bf16x2(v[t].z, v[t].w)};
+              ss = v[t].x * v[t].x + v[t].y * v[t].y + v[t].z * v[t].z + v[t].w * v[t].w;
             }
           } else if (col + 3 < p.n_valid && p.vec_ok) {
-            *reinterpret_cast<f32x4_t*>(o) = v;
+            *reinterpret_cast<f32x4_t*>(o) = v[t];
           } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              if (col + e < p.n_valid) o[e] = v[e];
+              if (col + e < p.n_valid) o[e] = v[t][e];
           }
         }
         if (p.ss_out) {
-          // CPR == 16: lanes 16k .. 16k + 15 hold the 64 columns of one row
-          static_assert(C::WTN == 64, "norm partial sums are per 64 columns");
+          // CPR is a multiple of 16: lanes 16k .. 16k + 15 hold one aligned
+          // 64-column group of one row
+          static_assert(C::WTN % 64 == 0, "norm partial sums are per 64 columns");
           ss = sum16(ss);
-          if (c == 0 && ok) p.ss_out[row * p.ss_np + col0 / 64] = ss;
+          if ((c & 15) == 0 && ok) p.ss_out[row * p.ss_np + (col0 + c * 4) / 64] = ss;
         }
       }
       wave_lds_fence();
     }
-    return;
-  }
+  } else {
   // bf16 outputs: BF16 (WTN columns), QKV_ROPE (WTN), SILU_GATE (WTN / 2)
-  const bool silu = p.epi == EPI_SILU_GATE;
+  constexpr bool silu = EPI == EPI_SILU_GATE;
+  // rope_cols % 64 == 0: each 64-column head is rotated or not as a whole
+  const bool rope = EPI == EPI_QKV_ROPE && col0 < p.rope_cols;
   constexpr int LD = C::WTN + 4;  // bf16 row pitch (8-byte pad)
   uint16_t* buf = reinterpret_cast<uint16_t*>(smem) + wid * 64 * LD;
+  // RoPE (cos, sin) pairs of this lane's 16 frequencies (8 g + 4 lhalf + e)
+  // for its row of tile row i, loaded one row ahead
+  f32x4_t cscur[8], csnext[8];
+  auto load_cs = [&](int i) {
+    const int64_t pos = rope_pos(p, row0 + i * 32 + lrow);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float* cs = p.rope_cs + (pos * 32 + 8 * g + 4 * lhalf) * 2;
+      csnext[2 * g] = *reinterpret_cast<const f32x4_t*>(cs);
+      csnext[2 * g + 1] = *reinterpret_cast<const f32x4_t*>(cs + 4);
+    }
+  };
+  if (rope) load_cs(0);
 #pragma unroll
   for (int i0 = 0; i0 < C::TM; i0 += 2) {
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
       const int i = i0 + ii;
       const int rl = ii * 32 + lrow;  // row within this 64-row slab
-      const int64_t row = row0 + i * 32 + lrow;
-      const int64_t pos = p.epi != EPI_QKV_ROPE ? 0 : rope_pos(p, row);
-      if (p.epi == EPI_BF16) {
+      if constexpr (EPI == EPI_BF16) {
 #pragma unroll
         for (int j = 0; j < C::TN; ++j)
 #pragma unroll
           for (int g = 0; g < 4; ++g)
             *reinterpret_cast<u32x2_t*>(buf + rl * LD + j * 32 + 8 * g + 4 * lhalf) =
-                u32x2_t{pack_bf16x2(acc[i][j][4 * g], acc[i][j][4 * g + 1]),
-                        pack_bf16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3])};
+                u32x2_t{pack_bf16x2(acc[i][j][4 * g] * rs[i], acc[i][j][4 * g + 1] * rs[i]),
+                        pack_bf16x2(acc[i][j][4 * g + 2] * rs[i], acc[i][j][4 * g + 3] * rs[i])};
         continue;
+      }
+      if (rope) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) cscur[t] = csnext[t];
+        if (i + 1 < C::TM) load_cs(i + 1);
       }
 #pragma unroll
       for (int j = 0; j < C::TN; j += 2)
@@ -483,21 +525,24 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
           float x1[4], x2[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            x1[e] = acc[i][j][4 * g + e];
-            x2[e] = acc[i][j + 1][4 * g + e];
+            x1[e] = acc[i][j][4 * g + e] * rs[i];
+            x2[e] = acc[i][j + 1][4 * g + e] * rs[i];
           }
           if (silu) {
+            // silu(g) * u = g / (1 + e^-g) * u, with the hardware exp2 and
+            // reciprocal (about 1 ulp each)
             float o[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = (x1[e] / (1.f + __expf(-x1[e]))) * x2[e];
+            for (int e = 0; e < 4; ++e)
+              o[e] = x1[e] *
+                     __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x1[e] * 1.44269504f)) *
+                     x2[e];
             *reinterpret_cast<u32x2_t*>(buf + rl * LD + (j / 2) * 32 + 8 * g + 4 * lhalf) =
                 u32x2_t{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
           } else {
             float o1[4], o2[4];
-            if (col0 + cl < p.rope_cols) {
-              const float* cs = p.rope_cs + (pos * 32 + (cl & 31)) * 2;
-              const f32x4_t c01 = *reinterpret_cast<const f32x4_t*>(cs);
-              const f32x4_t c23 = *reinterpret_cast<const f32x4_t*>(cs + 4);
+            if (rope && col0 + j * 32 < p.rope_cols) {
+              const f32x4_t c01 = cscur[2 * g], c23 = cscur[2 * g + 1];
               const float cv[4] = {c01.x, c01.z, c23.x, c23.z};
               const float sv[4] = {c01.y, c01.w, c23.y, c23.w};
 #pragma unroll
@@ -536,6 +581,7 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
     }
     wave_lds_fence();
   }
+  }
 }
 
 // 16 bytes per lane from global memory straight into LDS (gfx950
@@ -569,7 +615,7 @@ __device__ inline void dma_wait_barrier() {
 // 1-KB DMA chunks per K tile; a chunk is RPC LDS rows of BK bf16, and lane i
 // fetches the global 16-byte piece that the swizzle places at row i / CH,
 // slot i % CH.
-template <int BM, int BN, int BK, int WM, int WN, int S, int OCC>
+template <int BM, int BN, int BK, int WM, int WN, int S, int OCC, int EPI>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(OCC)))
 void gemm_bf16_dma_kernel(GemmArgs p) {
   using C = GemmCfg<BM, BN, BK, WM, WN>;
@@ -689,7 +735,313 @@ void gemm_bf16_dma_kernel(GemmArgs p) {
 
   // every wave is past its last LDS read of the K loop before LDS is reused
   __syncthreads();
-  epilogue_lds<C>(p, acc, m0, n0, wid, wm, wn, lane, reinterpret_cast<unsigned char*>(lds), rs);
+  epilogue_lds<C, EPI>(p, acc, m0, n0, wid, wm, wn, lane, reinterpret_cast<unsigned char*>(lds), rs);
+}
+
+
+// ---- 8-wave ping-pong schedule.  The per-CU vector memory path accepts about
+// 64 bytes per clock, so when all waves of a block issue their K-tile copies
+// at once they queue behind each other and no wave issues MFMAs meanwhile.
+// Here the two waves that share a SIMD belong to different groups (waves 0-3
+// and 4-7) and alternate roles: in its memory phase a wave issues its share of
+// the LDS-DMA copies of K tile k + S - 1 and reads all its fragments of K tile k
+// from LDS into registers; in its compute phase it runs the MFMAs of that tile
+// from registers only.  A block barrier ends every phase and group 1 starts one
+// phase late, so each SIMD always has one wave feeding its MFMA pipe.  Wave
+// (wm, wn) covers the same 128 x 64 sub-tile as in the 2 x 4 layout of
+// gemm_bf16_dma_kernel (group g owns columns [g BN/2, (g+1) BN/2)), so the
+// epilogue is shared.
+//
+// Ordering (barrier b(j) ends phase j; group 0 runs memory(k) in phase 2k,
+// group 1 in phase 2k + 1):
+//  - tile k is read from phase 2k on, so every wave has waited for its own
+//    copies of tile k before b(2k - 1), the barrier both groups cross last
+//    before phase 2k (group 0 after compute(k - 1), group 1 after
+//    memory(k - 1));
+//  - tile k + S - 1 goes into the stage of tile k - 1, whose last reader is
+//    group 1's memory(k - 1) in phase 2k - 1; its copies are issued in phase 2k
+//    (group 0) and 2k + 1 (group 1), after that phase's barrier, and every
+//    memory phase ends with its LDS reads complete.
+template <int BM, int BN, int BK, int S, int EPI>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
+void gemm_bf16_pp_kernel(GemmArgs p) {
+  constexpr int WM = 2, WN = 4, NW = 8;
+  using C = GemmCfg<BM, BN, BK, WM, WN>;
+  constexpr int RPC = 64 / C::CH;        // LDS rows per 1-KB chunk
+  constexpr int RPB = 128 / BK;          // rows per 256 bytes (swizzle period)
+  constexpr int NCH = (BM + BN) / RPC;   // 1-KB chunks per stage
+  constexpr int NI = NCH / NW;           // chunks per wave per stage
+  constexpr int D = S - 1;               // K tiles in flight ahead of the one read
+  constexpr int KS = BK / 16;            // MFMA K steps per K tile
+  static_assert(NCH % NW == 0, "DMA chunks must divide over the waves");
+  static_assert(S >= 3, "the ping-pong needs at least three LDS stages");
+  static_assert(NW * 64 * (C::WTN + 4) * 2 <= S * C::STAGE * 2 &&
+                    NW * 32 * (C::WTN + 2) * 4 <= S * C::STAGE * 2,
+                "staged epilogue must fit in the K-loop LDS");
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[S * C::STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int grp = wid >> 2, wi = wid & 3;
+  const int wm = wi >> 1, wn = (wi & 1) + 2 * grp;
+  int64_t m0, n0;
+  tile_origin<BM, BN>(p, m0, n0);
+  const int64_t am = p.M - 1 - m0, bn = p.N - 1 - n0;
+  const unsigned lds_base = (unsigned)(uintptr_t)lds;
+
+  const uint16_t* gsrc[NI];
+  unsigned lofs[NI];
+#pragma unroll
+  for (int q = 0; q < NI; ++q) {
+    const int ci = wid * NI + q;
+    const bool isA = ci < BM / RPC;  // uniform
+    const int rb = (isA ? ci : ci - BM / RPC) * RPC;
+    const int r = rb + lane / C::CH;
+    const int c = (lane % C::CH) ^ ((r / RPB) & (C::CH - 1));
+    const uint16_t* base = isA ? p.A : p.Bt;
+    const int64_t ld = isA ? p.lda : p.ldb;
+    const int64_t row = isA ? m0 + (r < am ? r : am) : n0 + (r < bn ? r : bn);
+    gsrc[q] = base + row * ld + c * 8;
+    lofs[q] = (isA ? 0u : (unsigned)(BM * BK * 2)) + (unsigned)(rb * BK * 2);
+  }
+  auto dma_tile = [&](int kt, int stage) {
+    const int64_t k0 = (int64_t)kt * BK;
+    const unsigned sbase = lds_base + (unsigned)(stage * C::STAGE * 2);
+#pragma unroll
+    for (int q = 0; q < NI; ++q)
+      dma16(gsrc[q] + k0, __builtin_amdgcn_readfirstlane(sbase + lofs[q]));
+  };
+  // at most NI * n of this wave's copies still in flight (n < D)
+  auto wait_copies = [&](int n) {
+    static_for<0, D>([&](auto ic) {
+      if (n == decltype(ic)::value)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NI * decltype(ic)::value) : "memory");
+    });
+  };
+  auto barrier = [] {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  f32x16_t acc[C::TM][C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  bf16x8_t af[KS][C::TM], bfr[KS][C::TN];
+  auto read_frags = [&](int stage) {
+    const uint16_t* sa = lds + stage * C::STAGE;
+    const uint16_t* sb = sa + BM * BK;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int chunk = ks * 2 + lhalf;
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+        af[ks][i] =
+            *reinterpret_cast<const bf16x8_t*>(sa + swz<BK>(wm * C::WTM + i * 32 + lrow, chunk));
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+        bfr[ks][j] =
+            *reinterpret_cast<const bf16x8_t*>(sb + swz<BK>(wn * C::WTN + j * 32 + lrow, chunk));
+    }
+  };
+  auto mfmas = [&] {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks][j], af[ks][i], acc[i][j], 0,
+                                                              0, 0);
+  };
+
+  const int KT = (int)(p.K / BK);
+  const int pre = KT < D ? KT : D;  // tiles issued before the loop
+  for (int t = 0; t < pre; ++t) dma_tile(t, t);
+  float rs[C::TM];
+  load_row_scales<C>(p, m0 + wm * C::WTM + lrow, rs);
+  wait_copies(pre - 1);  // this wave's copies of tile 0 have landed
+  barrier();             // ... and everyone's
+  if (grp == 1) barrier();  // group 1 runs one phase behind
+  int st = 0;  // stage of tile k
+  for (int k = 0; k < KT; ++k) {
+    // memory phase
+    if (k + D < KT) dma_tile(k + D, st == 0 ? S - 1 : st - 1);
+    read_frags(st);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int newest = k + D < KT - 1 ? k + D : KT - 1;
+    if (grp == 1 && k + 1 < KT) wait_copies(newest - (k + 1));
+    barrier();
+    // compute phase
+    mfmas();
+    if (grp == 0 && k + 1 < KT) wait_copies(newest - (k + 1));
+    barrier();
+    st = st + 1 < S ? st + 1 : 0;
+  }
+  if (grp == 0) barrier();  // matches group 1's extra barrier at the start
+
+  // all copies have landed and all LDS reads are complete: LDS is free
+  epilogue_lds<C, EPI>(p, acc, m0, n0, wid, wm, wn, lane, reinterpret_cast<unsigned char*>(lds), rs);
+}
+
+
+// ---- 4-wave schedule, 128 x 128 wave tiles.  LDS bandwidth is what limits
+// the 8-wave layouts above: per MFMA they read 0.75 KB of fragments (6 reads
+// per 8 MFMAs) besides the DMA writes.  Here each of the 4 waves (one per
+// SIMD) owns a 128 x 128 sub-tile of the 256 x 256 block tile, 16 f32x16
+// accumulators (AGPRs), and reads 8 fragments per 16 MFMAs.  With one wave
+// per SIMD any wait in its instruction stream idles the MFMA pipe, so the
+// loop is branch-free and everything else rides between the MFMAs: per K
+// step of 16, the 16 MFMAs of the current fragment set carry the 8 LDS reads
+// of the next set (issued first, so they complete long before they are
+// needed) and 4 of the wave's LDS-DMA copies.
+//
+// K tiles of BK = 32 (two K steps) move through S = 4 LDS stages; tile
+// kt + 3 is copied during tile kt into the stage of tile kt - 1.  Past the
+// last tile the copies repeat tile KT - 1 into stages nobody reads again, so
+// every tile issues the same copies and waits for the same count.  One barrier
+// per K tile, between its two K steps:
+//  - before it, every wave has finished reading tile kt (its second K step's
+//    fragments were read during the first) and has waited for its own copies
+//    of tile kt + 1 (the copies of kt + 2 and the first half of kt + 3 may
+//    still be in flight);
+//  - after it, the second K step reads tile kt + 1's first fragments, and the
+//    next tile's copies may overwrite the stage of tile kt.
+template <int BM, int BN, int BK, int S, int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+void gemm_bf16_w4_kernel(GemmArgs p) {
+  constexpr int WM = 2, WN = 2, NW = 4;
+  using C = GemmCfg<BM, BN, BK, WM, WN>;
+  constexpr int RPC = 64 / C::CH;        // LDS rows per 1-KB chunk
+  constexpr int RPB = 128 / BK;          // rows per 256 bytes (swizzle period)
+  constexpr int NCH = (BM + BN) / RPC;   // 1-KB chunks per stage
+  constexpr int NI = NCH / NW;           // chunks per wave per stage
+  constexpr int KS = BK / 16;            // K steps per K tile
+  constexpr int NIK = NI / KS;           // copies interleaved per K step
+  constexpr int NMF = C::TM * C::TN;     // MFMAs per K step
+  constexpr int NFR = C::TM + C::TN;     // fragment reads per K step
+  static_assert(KS == 2, "the barrier sits between the two K steps of a tile");
+  static_assert(S == 4, "tile kt + 3 is copied during tile kt");
+  static_assert(NCH % NW == 0 && NI % KS == 0, "DMA chunks must divide over waves and K steps");
+  static_assert(NFR <= NMF / 2 && NMF == 4 * NIK,
+                "interleave: reads in the first half, a copy every 4 MFMAs");
+  static_assert(NW * 64 * (C::WTN + 4) * 2 <= S * C::STAGE * 2 &&
+                    NW * 32 * (C::WTN + 2) * 4 <= S * C::STAGE * 2,
+                "staged epilogue must fit in the K-loop LDS");
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[S * C::STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int wm = wid >> 1, wn = wid & 1;
+  int64_t m0, n0;
+  tile_origin<BM, BN>(p, m0, n0);
+  const int64_t am = p.M - 1 - m0, bn = p.N - 1 - n0;
+  const unsigned lds_base = (unsigned)(uintptr_t)lds;
+
+  const uint16_t* gsrc[NI];
+  unsigned lofs[NI];
+#pragma unroll
+  for (int q = 0; q < NI; ++q) {
+    const int ci = wid * NI + q;
+    const bool isA = ci < BM / RPC;  // uniform
+    const int rb = (isA ? ci : ci - BM / RPC) * RPC;
+    const int r = rb + lane / C::CH;
+    const int c = (lane % C::CH) ^ ((r / RPB) & (C::CH - 1));
+    const uint16_t* base = isA ? p.A : p.Bt;
+    const int64_t ld = isA ? p.lda : p.ldb;
+    const int64_t row = isA ? m0 + (r < am ? r : am) : n0 + (r < bn ? r : bn);
+    gsrc[q] = base + row * ld + c * 8;
+    lofs[q] = (isA ? 0u : (unsigned)(BM * BK * 2)) + (unsigned)(rb * BK * 2);
+  }
+  const int KT = (int)(p.K / BK);
+  // copy q of K tile kt (clamped to the last tile) into `stage`
+  auto dma_chunk = [&](int q, int kt, int stage) {
+    const int t = kt < KT ? kt : KT - 1;
+    dma16(gsrc[q] + (int64_t)t * BK,
+          __builtin_amdgcn_readfirstlane(lds_base + (unsigned)(stage * C::STAGE * 2) + lofs[q]));
+  };
+
+  f32x16_t acc[C::TM][C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  bf16x8_t fa[2][C::TM], fb[2][C::TN];  // fragment sets of two consecutive K steps
+  // fragment f (A rows for f < TM, else Bt rows) of K step ks of the tile in
+  // `stage`, in the order the MFMAs consume them (A0, B0 .. B3, A1 .. A3)
+  auto read_frag = [&](auto setc, auto fc, int stage, int ks) {
+    constexpr int SET = decltype(setc)::value, F0 = decltype(fc)::value;
+    constexpr int F = F0 == 0 ? 0 : (F0 <= C::TN ? C::TM + F0 - 1 : F0 - C::TN);
+    const uint16_t* sa = lds + stage * C::STAGE;
+    const int chunk = ks * 2 + lhalf;
+    if constexpr (F < C::TM)
+      fa[SET][F] = *reinterpret_cast<const bf16x8_t*>(
+          sa + swz<BK>(wm * C::WTM + F * 32 + lrow, chunk));
+    else
+      fb[SET][F - C::TM] = *reinterpret_cast<const bf16x8_t*>(
+          sa + BM * BK + swz<BK>(wn * C::WTN + (F - C::TM) * 32 + lrow, chunk));
+  };
+  // The NMF MFMAs of fragment set CUR, interleaved with the reads of the next
+  // K step's fragments (K step rks of the tile in rstage) into the other set
+  // and with copies q0 .. q0 + NIK - 1 of tile dkt into dstage.
+  auto kstep = [&](auto curc, int rstage, int rks, int dkt, int dstage, int q0) {
+    constexpr int CUR = decltype(curc)::value;
+    static_for<0, NMF>([&](auto mc) {
+      constexpr int m = decltype(mc)::value;
+      acc[m / C::TN][m % C::TN] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          fb[CUR][m % C::TN], fa[CUR][m / C::TN], acc[m / C::TN][m % C::TN], 0, 0, 0);
+      if constexpr (m < NFR)
+        read_frag(std::integral_constant<int, CUR ^ 1>{}, std::integral_constant<int, m>{},
+                  rstage, rks);
+      if constexpr (m % 4 == 1) dma_chunk(q0 + m / 4, dkt, dstage);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+  auto barrier = [] {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // prologue: tiles 0, 1, 2 in flight; wait for this wave's copies of tile 0
+#pragma unroll
+  for (int t = 0; t < S - 1; ++t)
+#pragma unroll
+    for (int q = 0; q < NI; ++q) dma_chunk(q, t, t);
+  float rs[C::TM];
+  load_row_scales<C>(p, m0 + wm * C::WTM + lrow, rs);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NI) : "memory");
+  barrier();
+  static_for<0, NFR>([&](auto fc) { read_frag(std::integral_constant<int, 0>{}, fc, 0, 0); });
+
+  int st = 0;  // stage of tile kt
+  for (int kt = 0; kt < KT; ++kt) {
+    const int nst = st + 1 < S ? st + 1 : 0;   // stage of tile kt + 1
+    const int dst = st == 0 ? S - 1 : st - 1;  // stage of tile kt + 3 (= kt - 1)
+    // K step 0 of tile kt; reads K step 1 of tile kt
+    kstep(std::integral_constant<int, 0>{}, st, 1, kt + S - 1, dst, 0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)" ::"n"(NI + NIK) : "memory");
+    barrier();
+    // K step 1 of tile kt; reads K step 0 of tile kt + 1 (past the last tile
+    // these reads land in registers that are never used)
+    kstep(std::integral_constant<int, 1>{}, nst, 0, kt + S - 1, dst, NIK);
+    st = nst;
+  }
+
+  // every copy has landed and every wave is past its last LDS read
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  epilogue_lds<C, EPI>(p, acc, m0, n0, wid, wm, wn, lane, reinterpret_cast<unsigned char*>(lds), rs);
 }
 
 }  // namespace gemm

@@ -4,13 +4,26 @@
 namespace blt {
 
 namespace {
-template <int BM, int BN, int BK, int WM, int WN, int S, int OCC>
+template <int BM, int BN, int BK, int WM, int WN, int S, int OCC, int EPI>
 int run_gemm_dma(const GemmArgs& a, hipStream_t s) {
   const int64_t nb = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm::gemm_bf16_dma_kernel<BM, BN, BK, WM, WN, S, OCC>), dim3((unsigned)nb),
-                     dim3(64 * WM * WN), 0, s, a);
+  hipLaunchKernelGGL((gemm::gemm_bf16_dma_kernel<BM, BN, BK, WM, WN, S, OCC, EPI>),
+                     dim3((unsigned)nb), dim3(64 * WM * WN), 0, s, a);
   BLT_LAUNCH_CHECK("gemm_bf16_dma_kernel");
   return 0;
+}
+
+// one kernel per epilogue, so each carries only its own registers and code
+template <int BM, int BN, int BK, int WM, int WN, int S, int OCC>
+int run_gemm_dma_epi(const GemmArgs& a, hipStream_t s) {
+  switch (a.epi) {
+    case EPI_BF16: return run_gemm_dma<BM, BN, BK, WM, WN, S, OCC, EPI_BF16>(a, s);
+    case EPI_F32: return run_gemm_dma<BM, BN, BK, WM, WN, S, OCC, EPI_F32>(a, s);
+    case EPI_RESID_F32: return run_gemm_dma<BM, BN, BK, WM, WN, S, OCC, EPI_RESID_F32>(a, s);
+    case EPI_QKV_ROPE: return run_gemm_dma<BM, BN, BK, WM, WN, S, OCC, EPI_QKV_ROPE>(a, s);
+    case EPI_SILU_GATE: return run_gemm_dma<BM, BN, BK, WM, WN, S, OCC, EPI_SILU_GATE>(a, s);
+  }
+  return fail(-2, "gemm: unknown epilogue");
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int PF, int OCC>
@@ -44,7 +57,7 @@ int launch_gemm(const GemmArgs& a_in, hipStream_t s) {
   // N % 256 == 0: 256x256 tiles over 8 waves (wave tile 128x64), K tiles of
   // 64 moved by LDS DMA through 2 stages, LDS-staged epilogue.  Otherwise (the
   // 260-wide head) 128x128 register-staged tiles over 4 waves.
-  if (a.N % 256 == 0) return run_gemm_dma<256, 256, 64, 2, 4, 2, 2>(a, s);
+  if (a.N % 256 == 0) return run_gemm_dma_epi<256, 256, 64, 2, 4, 2, 2>(a, s);
   return run_gemm<128, 128, 32, 2, 2, 2, 3>(a, s);
 }
 
