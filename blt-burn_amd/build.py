@@ -21,12 +21,16 @@ FLAGS = [
     "-mcode-object-version=5",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-ffp-contract=fast", "-Wall", "-Wno-unused-function",
-    # keep MFMA sources and results in arch VGPRs: the attention softmax works
-    # on the score accumulators with VALU ops, and results parked in AGPRs cost
-    # a v_accvgpr read/write per value per tile
-    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", os.path.join(HERE, "..", "include"),
 ]
+# per-file additions
+FILE_FLAGS = {
+    # keep MFMA sources and results in arch VGPRs: the attention softmax works
+    # on the score accumulators with VALU ops, and results parked in AGPRs cost
+    # a v_accvgpr read/write per value per tile (the GEMMs keep their
+    # accumulators in AGPRs where the 4-wave tiles need the room)
+    "k_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
 
 
 def _run(cmd):
@@ -41,7 +45,8 @@ def build(verbose=False):
     os.makedirs(OBJ, exist_ok=True)
     srcs = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
     objs = [os.path.join(OBJ, f[:-4] + ".o") for f in srcs]
-    jobs = [[HIPCC] + FLAGS + ["-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(srcs, objs)]
+    jobs = [[HIPCC] + FLAGS + FILE_FLAGS.get(s, []) + ["-c", os.path.join(CSRC, s), "-o", o]
+            for s, o in zip(srcs, objs)]
     with ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
         for out in ex.map(_run, jobs):
             if verbose and out.strip():

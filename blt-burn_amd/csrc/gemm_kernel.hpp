@@ -739,310 +739,5 @@ void gemm_bf16_dma_kernel(GemmArgs p) {
 }
 
 
-// ---- 8-wave ping-pong schedule.  The per-CU vector memory path accepts about
-// 64 bytes per clock, so when all waves of a block issue their K-tile copies
-// at once they queue behind each other and no wave issues MFMAs meanwhile.
-// Here the two waves that share a SIMD belong to different groups (waves 0-3
-// and 4-7) and alternate roles: in its memory phase a wave issues its share of
-// the LDS-DMA copies of K tile k + S - 1 and reads all its fragments of K tile k
-// from LDS into registers; in its compute phase it runs the MFMAs of that tile
-// from registers only.  A block barrier ends every phase and group 1 starts one
-// phase late, so each SIMD always has one wave feeding its MFMA pipe.  Wave
-// (wm, wn) covers the same 128 x 64 sub-tile as in the 2 x 4 layout of
-// gemm_bf16_dma_kernel (group g owns columns [g BN/2, (g+1) BN/2)), so the
-// epilogue is shared.
-//
-// Ordering (barrier b(j) ends phase j; group 0 runs memory(k) in phase 2k,
-// group 1 in phase 2k + 1):
-//  - tile k is read from phase 2k on, so every wave has waited for its own
-//    copies of tile k before b(2k - 1), the barrier both groups cross last
-//    before phase 2k (group 0 after compute(k - 1), group 1 after
-//    memory(k - 1));
-//  - tile k + S - 1 goes into the stage of tile k - 1, whose last reader is
-//    group 1's memory(k - 1) in phase 2k - 1; its copies are issued in phase 2k
-//    (group 0) and 2k + 1 (group 1), after that phase's barrier, and every
-//    memory phase ends with its LDS reads complete.
-template <int BM, int BN, int BK, int S, int EPI>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
-void gemm_bf16_pp_kernel(GemmArgs p) {
-  constexpr int WM = 2, WN = 4, NW = 8;
-  using C = GemmCfg<BM, BN, BK, WM, WN>;
-  constexpr int RPC = 64 / C::CH;        // LDS rows per 1-KB chunk
-  constexpr int RPB = 128 / BK;          // rows per 256 bytes (swizzle period)
-  constexpr int NCH = (BM + BN) / RPC;   // 1-KB chunks per stage
-  constexpr int NI = NCH / NW;           // chunks per wave per stage
-  constexpr int D = S - 1;               // K tiles in flight ahead of the one read
-  constexpr int KS = BK / 16;            // MFMA K steps per K tile
-  static_assert(NCH % NW == 0, "DMA chunks must divide over the waves");
-  static_assert(S >= 3, "the ping-pong needs at least three LDS stages");
-  static_assert(NW * 64 * (C::WTN + 4) * 2 <= S * C::STAGE * 2 &&
-                    NW * 32 * (C::WTN + 2) * 4 <= S * C::STAGE * 2,
-                "staged epilogue must fit in the K-loop LDS");
-  __shared__ __attribute__((aligned(1024))) uint16_t lds[S * C::STAGE];
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-  const int grp = wid >> 2, wi = wid & 3;
-  const int wm = wi >> 1, wn = (wi & 1) + 2 * grp;
-  int64_t m0, n0;
-  tile_origin<BM, BN>(p, m0, n0);
-  const int64_t am = p.M - 1 - m0, bn = p.N - 1 - n0;
-  const unsigned lds_base = (unsigned)(uintptr_t)lds;
-
-  const uint16_t* gsrc[NI];
-  unsigned lofs[NI];
-#pragma unroll
-  for (int q = 0; q < NI; ++q) {
-    const int ci = wid * NI + q;
-    const bool isA = ci < BM / RPC;  // uniform
-    const int rb = (isA ? ci : ci - BM / RPC) * RPC;
-    const int r = rb + lane / C::CH;
-    const int c = (lane % C::CH) ^ ((r / RPB) & (C::CH - 1));
-    const uint16_t* base = isA ? p.A : p.Bt;
-    const int64_t ld = isA ? p.lda : p.ldb;
-    const int64_t row = isA ? m0 + (r < am ? r : am) : n0 + (r < bn ? r : bn);
-    gsrc[q] = base + row * ld + c * 8;
-    lofs[q] = (isA ? 0u : (unsigned)(BM * BK * 2)) + (unsigned)(rb * BK * 2);
-  }
-  auto dma_tile = [&](int kt, int stage) {
-    const int64_t k0 = (int64_t)kt * BK;
-    const unsigned sbase = lds_base + (unsigned)(stage * C::STAGE * 2);
-#pragma unroll
-    for (int q = 0; q < NI; ++q)
-      dma16(gsrc[q] + k0, __builtin_amdgcn_readfirstlane(sbase + lofs[q]));
-  };
-  // at most NI * n of this wave's copies still in flight (n < D)
-  auto wait_copies = [&](int n) {
-    static_for<0, D>([&](auto ic) {
-      if (n == decltype(ic)::value)
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NI * decltype(ic)::value) : "memory");
-    });
-  };
-  auto barrier = [] {
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_barrier" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  f32x16_t acc[C::TM][C::TN];
-#pragma unroll
-  for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  const int lrow = lane & 31, lhalf = lane >> 5;
-  bf16x8_t af[KS][C::TM], bfr[KS][C::TN];
-  auto read_frags = [&](int stage) {
-    const uint16_t* sa = lds + stage * C::STAGE;
-    const uint16_t* sb = sa + BM * BK;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int chunk = ks * 2 + lhalf;
-#pragma unroll
-      for (int i = 0; i < C::TM; ++i)
-        af[ks][i] =
-            *reinterpret_cast<const bf16x8_t*>(sa + swz<BK>(wm * C::WTM + i * 32 + lrow, chunk));
-#pragma unroll
-      for (int j = 0; j < C::TN; ++j)
-        bfr[ks][j] =
-            *reinterpret_cast<const bf16x8_t*>(sb + swz<BK>(wn * C::WTN + j * 32 + lrow, chunk));
-    }
-  };
-  auto mfmas = [&] {
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks][j], af[ks][i], acc[i][j], 0,
-                                                              0, 0);
-  };
-
-  const int KT = (int)(p.K / BK);
-  const int pre = KT < D ? KT : D;  // tiles issued before the loop
-  for (int t = 0; t < pre; ++t) dma_tile(t, t);
-  float rs[C::TM];
-  load_row_scales<C>(p, m0 + wm * C::WTM + lrow, rs);
-  wait_copies(pre - 1);  // this wave's copies of tile 0 have landed
-  barrier();             // ... and everyone's
-  if (grp == 1) barrier();  // group 1 runs one phase behind
-  int st = 0;  // stage of tile k
-  for (int k = 0; k < KT; ++k) {
-    // memory phase
-    if (k + D < KT) dma_tile(k + D, st == 0 ? S - 1 : st - 1);
-    read_frags(st);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    const int newest = k + D < KT - 1 ? k + D : KT - 1;
-    if (grp == 1 && k + 1 < KT) wait_copies(newest - (k + 1));
-    barrier();
-    // compute phase
-    mfmas();
-    if (grp == 0 && k + 1 < KT) wait_copies(newest - (k + 1));
-    barrier();
-    st = st + 1 < S ? st + 1 : 0;
-  }
-  if (grp == 0) barrier();  // matches group 1's extra barrier at the start
-
-  // all copies have landed and all LDS reads are complete: LDS is free
-  epilogue_lds<C, EPI>(p, acc, m0, n0, wid, wm, wn, lane, reinterpret_cast<unsigned char*>(lds), rs);
-}
-
-
-// ---- 4-wave schedule, 128 x 128 wave tiles.  LDS bandwidth is what limits
-// the 8-wave layouts above: per MFMA they read 0.75 KB of fragments (6 reads
-// per 8 MFMAs) besides the DMA writes.  Here each of the 4 waves (one per
-// SIMD) owns a 128 x 128 sub-tile of the 256 x 256 block tile, 16 f32x16
-// accumulators (AGPRs), and reads 8 fragments per 16 MFMAs.  With one wave
-// per SIMD any wait in its instruction stream idles the MFMA pipe, so the
-// loop is branch-free and everything else rides between the MFMAs: per K
-// step of 16, the 16 MFMAs of the current fragment set carry the 8 LDS reads
-// of the next set (issued first, so they complete long before they are
-// needed) and 4 of the wave's LDS-DMA copies.
-//
-// K tiles of BK = 32 (two K steps) move through S = 4 LDS stages; tile
-// kt + 3 is copied during tile kt into the stage of tile kt - 1.  Past the
-// last tile the copies repeat tile KT - 1 into stages nobody reads again, so
-// every tile issues the same copies and waits for the same count.  One barrier
-// per K tile, between its two K steps:
-//  - before it, every wave has finished reading tile kt (its second K step's
-//    fragments were read during the first) and has waited for its own copies
-//    of tile kt + 1 (the copies of kt + 2 and the first half of kt + 3 may
-//    still be in flight);
-//  - after it, the second K step reads tile kt + 1's first fragments, and the
-//    next tile's copies may overwrite the stage of tile kt.
-template <int BM, int BN, int BK, int S, int EPI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
-void gemm_bf16_w4_kernel(GemmArgs p) {
-  constexpr int WM = 2, WN = 2, NW = 4;
-  using C = GemmCfg<BM, BN, BK, WM, WN>;
-  constexpr int RPC = 64 / C::CH;        // LDS rows per 1-KB chunk
-  constexpr int RPB = 128 / BK;          // rows per 256 bytes (swizzle period)
-  constexpr int NCH = (BM + BN) / RPC;   // 1-KB chunks per stage
-  constexpr int NI = NCH / NW;           // chunks per wave per stage
-  constexpr int KS = BK / 16;            // K steps per K tile
-  constexpr int NIK = NI / KS;           // copies interleaved per K step
-  constexpr int NMF = C::TM * C::TN;     // MFMAs per K step
-  constexpr int NFR = C::TM + C::TN;     // fragment reads per K step
-  static_assert(KS == 2, "the barrier sits between the two K steps of a tile");
-  static_assert(S == 4, "tile kt + 3 is copied during tile kt");
-  static_assert(NCH % NW == 0 && NI % KS == 0, "DMA chunks must divide over waves and K steps");
-  static_assert(NFR <= NMF / 2 && NMF == 4 * NIK,
-                "interleave: reads in the first half, a copy every 4 MFMAs");
-  static_assert(NW * 64 * (C::WTN + 4) * 2 <= S * C::STAGE * 2 &&
-                    NW * 32 * (C::WTN + 2) * 4 <= S * C::STAGE * 2,
-                "staged epilogue must fit in the K-loop LDS");
-  __shared__ __attribute__((aligned(1024))) uint16_t lds[S * C::STAGE];
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-  const int wm = wid >> 1, wn = wid & 1;
-  int64_t m0, n0;
-  tile_origin<BM, BN>(p, m0, n0);
-  const int64_t am = p.M - 1 - m0, bn = p.N - 1 - n0;
-  const unsigned lds_base = (unsigned)(uintptr_t)lds;
-
-  const uint16_t* gsrc[NI];
-  unsigned lofs[NI];
-#pragma unroll
-  for (int q = 0; q < NI; ++q) {
-    const int ci = wid * NI + q;
-    const bool isA = ci < BM / RPC;  // uniform
-    const int rb = (isA ? ci : ci - BM / RPC) * RPC;
-    const int r = rb + lane / C::CH;
-    const int c = (lane % C::CH) ^ ((r / RPB) & (C::CH - 1));
-    const uint16_t* base = isA ? p.A : p.Bt;
-    const int64_t ld = isA ? p.lda : p.ldb;
-    const int64_t row = isA ? m0 + (r < am ? r : am) : n0 + (r < bn ? r : bn);
-    gsrc[q] = base + row * ld + c * 8;
-    lofs[q] = (isA ? 0u : (unsigned)(BM * BK * 2)) + (unsigned)(rb * BK * 2);
-  }
-  const int KT = (int)(p.K / BK);
-  // copy q of K tile kt (clamped to the last tile) into `stage`
-  auto dma_chunk = [&](int q, int kt, int stage) {
-    const int t = kt < KT ? kt : KT - 1;
-    dma16(gsrc[q] + (int64_t)t * BK,
-          __builtin_amdgcn_readfirstlane(lds_base + (unsigned)(stage * C::STAGE * 2) + lofs[q]));
-  };
-
-  f32x16_t acc[C::TM][C::TN];
-#pragma unroll
-  for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  const int lrow = lane & 31, lhalf = lane >> 5;
-  bf16x8_t fa[2][C::TM], fb[2][C::TN];  // fragment sets of two consecutive K steps
-  // fragment f (A rows for f < TM, else Bt rows) of K step ks of the tile in
-  // `stage`, in the order the MFMAs consume them (A0, B0 .. B3, A1 .. A3)
-  auto read_frag = [&](auto setc, auto fc, int stage, int ks) {
-    constexpr int SET = decltype(setc)::value, F0 = decltype(fc)::value;
-    constexpr int F = F0 == 0 ? 0 : (F0 <= C::TN ? C::TM + F0 - 1 : F0 - C::TN);
-    const uint16_t* sa = lds + stage * C::STAGE;
-    const int chunk = ks * 2 + lhalf;
-    if constexpr (F < C::TM)
-      fa[SET][F] = *reinterpret_cast<const bf16x8_t*>(
-          sa + swz<BK>(wm * C::WTM + F * 32 + lrow, chunk));
-    else
-      fb[SET][F - C::TM] = *reinterpret_cast<const bf16x8_t*>(
-          sa + BM * BK + swz<BK>(wn * C::WTN + (F - C::TM) * 32 + lrow, chunk));
-  };
-  // The NMF MFMAs of fragment set CUR, interleaved with the reads of the next
-  // K step's fragments (K step rks of the tile in rstage) into the other set
-  // and with copies q0 .. q0 + NIK - 1 of tile dkt into dstage.
-  auto kstep = [&](auto curc, int rstage, int rks, int dkt, int dstage, int q0) {
-    constexpr int CUR = decltype(curc)::value;
-    static_for<0, NMF>([&](auto mc) {
-      constexpr int m = decltype(mc)::value;
-      acc[m / C::TN][m % C::TN] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-          fb[CUR][m % C::TN], fa[CUR][m / C::TN], acc[m / C::TN][m % C::TN], 0, 0, 0);
-      if constexpr (m < NFR)
-        read_frag(std::integral_constant<int, CUR ^ 1>{}, std::integral_constant<int, m>{},
-                  rstage, rks);
-      if constexpr (m % 4 == 1) dma_chunk(q0 + m / 4, dkt, dstage);
-      __builtin_amdgcn_sched_barrier(0);
-    });
-  };
-  auto barrier = [] {
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_barrier" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  // prologue: tiles 0, 1, 2 in flight; wait for this wave's copies of tile 0
-#pragma unroll
-  for (int t = 0; t < S - 1; ++t)
-#pragma unroll
-    for (int q = 0; q < NI; ++q) dma_chunk(q, t, t);
-  float rs[C::TM];
-  load_row_scales<C>(p, m0 + wm * C::WTM + lrow, rs);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NI) : "memory");
-  barrier();
-  static_for<0, NFR>([&](auto fc) { read_frag(std::integral_constant<int, 0>{}, fc, 0, 0); });
-
-  int st = 0;  // stage of tile kt
-  for (int kt = 0; kt < KT; ++kt) {
-    const int nst = st + 1 < S ? st + 1 : 0;   // stage of tile kt + 1
-    const int dst = st == 0 ? S - 1 : st - 1;  // stage of tile kt + 3 (= kt - 1)
-    // K step 0 of tile kt; reads K step 1 of tile kt
-    kstep(std::integral_constant<int, 0>{}, st, 1, kt + S - 1, dst, 0);
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)" ::"n"(NI + NIK) : "memory");
-    barrier();
-    // K step 1 of tile kt; reads K step 0 of tile kt + 1 (past the last tile
-    // these reads land in registers that are never used)
-    kstep(std::integral_constant<int, 1>{}, nst, 0, kt + S - 1, dst, NIK);
-    st = nst;
-  }
-
-  // every copy has landed and every wave is past its last LDS read
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  epilogue_lds<C, EPI>(p, acc, m0, n0, wid, wm, wn, lane, reinterpret_cast<unsigned char*>(lds), rs);
-}
-
 }  // namespace gemm
 }  // namespace blt
