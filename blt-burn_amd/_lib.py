@@ -42,6 +42,8 @@ EXPORTS = {
     "blt_rope_table_f32": (c_i32, [c_vp, c_i32, c_i32, c_f64, c_vp]),
     "blt_patch_boundaries": (c_i32, [c_vp, c_i64, c_i64, c_f32, c_i32, c_vp, c_vp, c_vp, c_vp,
                                      c_vp]),
+    "blt_patch_means": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp,
+                                c_vp]),
     "blt_model_create": (c_i32, [c_i32, c_vp, c_vp, c_i64, ctypes.POINTER(c_vp)]),
     "blt_model_destroy": (c_i32, [c_vp]),
     "blt_model_device_bytes": (c_i64, [c_vp]),
@@ -54,6 +56,7 @@ EXPORTS = {
     "blt_ingest_destroy": (c_i32, [c_vp]),
     "blt_ingest_last_stats": (c_i32, [c_vp, c_vp]),
     "blt_ingest_run": (c_i32, [c_vp, c_vp, c_vp, c_i64] + [c_vp] * 7),
+    "blt_ingest_run_patch_means": (c_i32, [c_vp, c_vp, c_vp, c_i64] + [c_vp] * 10),
     "blt_model_set_profiling": (c_i32, [c_vp, c_i32]),
     "blt_model_read_profile": (c_i32, [c_vp, ctypes.POINTER(c_f64), ctypes.POINTER(c_i64), c_i32]),
     "blt_stage_name": (ctypes.c_char_p, [c_i32]),

@@ -272,6 +272,21 @@ int blt_patch_boundaries(const float* H, int64_t B, int64_t T, float thr, int32_
                                  STREAM(stream));
 }
 
+int blt_patch_means(const float* entropies, const float* norms, const float* coherence,
+                    const int32_t* starts, const int32_t* count, int64_t B, int64_t T,
+                    float* mean_entropy, float* mean_prominence, float* mean_coherence,
+                    blt_stream_t stream) {
+  if (B < 0 || T < 0) return fail(BLT_ERR_SHAPE, "patch_means: negative shape");
+  if (T > 0x7fffffff) return fail(BLT_ERR_SHAPE, "patch_means: T must fit int32");
+  if ((coherence == nullptr) != (mean_coherence == nullptr))
+    return fail(BLT_ERR_INVALID, "patch_means: coherence and mean_coherence come as a pair");
+  if (B == 0) return BLT_OK;
+  if (!entropies || !norms || !starts || !count)
+    return fail(BLT_ERR_INVALID, "patch_means: null entropies, norms, starts or count");
+  return launch_patch_means(entropies, norms, coherence, starts, count, B, T, nullptr, nullptr,
+                            mean_entropy, mean_prominence, mean_coherence, STREAM(stream));
+}
+
 // ---- model -------------------------------------------------------------------
 int blt_model_create(int32_t device, const blt_model_config* cfg, const blt_model_weights* w,
                      int64_t max_tokens, blt_model** out) {

@@ -99,6 +99,9 @@ struct Ingest {
     int32_t* h_starts = nullptr;
     int32_t* h_lens = nullptr;
     int32_t* h_counts = nullptr;
+    float* h_pH = nullptr;  // per-patch means, document order
+    float* h_pN = nullptr;
+    float* h_pC = nullptr;
     // device
     int32_t* d_tok = nullptr;
     int32_t* d_seg = nullptr;
@@ -116,6 +119,9 @@ struct Ingest {
     int32_t* d_starts = nullptr;
     int32_t* d_lens = nullptr;
     int32_t* d_counts = nullptr;
+    float* d_pH = nullptr;
+    float* d_pN = nullptr;
+    float* d_pC = nullptr;
     hipEvent_t uploaded = nullptr, computed = nullptr, done = nullptr;
     bool busy = false;
     std::vector<int64_t> docs;  // caller's document ids in this batch
@@ -124,22 +130,30 @@ struct Ingest {
 
   ~Ingest();
   int init(Model* model, const blt_ingest_config& c);
+  // per-patch outputs of a run (document d's patches at doc_off[d] .. + counts[d])
+  struct PatchOut {
+    float* ent = nullptr;
+    float* prom = nullptr;
+    float* coh = nullptr;
+    bool any() const { return ent || prom || coh; }
+  };
   int run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, float* ent, float* nrm,
-          float* coh, float* emb, int32_t* starts, int32_t* lens, int32_t* counts);
+          float* coh, float* emb, int32_t* starts, int32_t* lens, int32_t* counts,
+          const PatchOut& pm);
   int finish(Slot& s, const int64_t* doc_off, float* ent, float* nrm, float* coh, float* emb,
-             int32_t* starts, int32_t* lens, int32_t* counts);
+             int32_t* starts, int32_t* lens, int32_t* counts, const PatchOut& pm);
 };
 
 Ingest::~Ingest() {
   for (Slot& s : slot) {
     if (s.busy && s.done) (void)hipEventSynchronize(s.done);
-    void* hp[] = {s.h_tok, s.h_seg, s.h_dest, s.h_doff,   s.h_dlen, s.h_H,
-                  s.h_N,   s.h_C,   s.h_E,    s.h_starts, s.h_lens, s.h_counts};
+    void* hp[] = {s.h_tok, s.h_seg, s.h_dest, s.h_doff,   s.h_dlen, s.h_H,    s.h_N,
+                  s.h_C,   s.h_E,   s.h_starts, s.h_lens, s.h_counts, s.h_pH, s.h_pN, s.h_pC};
     for (void* p : hp)
       if (p) (void)hipHostFree(p);
     void* dp[] = {s.d_tok, s.d_seg, s.d_dest, s.d_doff, s.d_dlen,   s.d_Hp,   s.d_Np,
                   s.d_Cp,  s.d_Ep,  s.d_H,    s.d_N,    s.d_C,      s.d_E,    s.d_starts,
-                  s.d_lens, s.d_counts};
+                  s.d_lens, s.d_counts, s.d_pH, s.d_pN, s.d_pC};
     for (void* p : dp)
       if (p) (void)hipFree(p);
     for (hipEvent_t e : {s.uploaded, s.computed, s.done})
@@ -180,11 +194,13 @@ int Ingest::init(Model* model, const blt_ingest_config& c) {
     HALLOC(s.h_doff, BT); HALLOC(s.h_dlen, BT);
     HALLOC(s.h_H, BT); HALLOC(s.h_N, BT); HALLOC(s.h_C, BT); HALLOC(s.h_E, ne);
     HALLOC(s.h_starts, BT); HALLOC(s.h_lens, BT); HALLOC(s.h_counts, BT);
+    HALLOC(s.h_pH, BT); HALLOC(s.h_pN, BT); HALLOC(s.h_pC, BT);
     DALLOC(s.d_tok, BT); DALLOC(s.d_seg, BT); DALLOC(s.d_dest, BT);
     DALLOC(s.d_doff, BT); DALLOC(s.d_dlen, BT);
     DALLOC(s.d_Hp, BT); DALLOC(s.d_Np, BT); DALLOC(s.d_Cp, BT); DALLOC(s.d_Ep, ne);
     DALLOC(s.d_H, BT); DALLOC(s.d_N, BT); DALLOC(s.d_C, BT); DALLOC(s.d_E, ne);
     DALLOC(s.d_starts, BT); DALLOC(s.d_lens, BT); DALLOC(s.d_counts, BT);
+    DALLOC(s.d_pH, BT); DALLOC(s.d_pN, BT); DALLOC(s.d_pC, BT);
 #undef HALLOC
 #undef DALLOC
     BLT_HIP_CHECK(hipEventCreateWithFlags(&s.uploaded, hipEventDisableTiming));
@@ -196,7 +212,8 @@ int Ingest::init(Model* model, const blt_ingest_config& c) {
 
 // Wait for a slot's batch and copy its per-document results to the caller.
 int Ingest::finish(Slot& s, const int64_t* doc_off, float* ent, float* nrm, float* coh,
-                   float* emb, int32_t* starts, int32_t* lens, int32_t* counts) {
+                   float* emb, int32_t* starts, int32_t* lens, int32_t* counts,
+                   const PatchOut& pm) {
   if (!s.busy) return 0;
   s.busy = false;
   BLT_HIP_CHECK(hipEventSynchronize(s.done));
@@ -211,6 +228,9 @@ int Ingest::finish(Slot& s, const int64_t* doc_off, float* ent, float* nrm, floa
     if (emb && s.h_E) memcpy(emb + dst * dim, s.h_E + src * dim, (size_t)(L * dim) * 4);
     if (starts) memcpy(starts + dst, s.h_starts + src, (size_t)n * 4);
     if (lens) memcpy(lens + dst, s.h_lens + src, (size_t)n * 4);
+    if (pm.ent) memcpy(pm.ent + dst, s.h_pH + src, (size_t)n * 4);
+    if (pm.prom) memcpy(pm.prom + dst, s.h_pN + src, (size_t)n * 4);
+    if (pm.coh) memcpy(pm.coh + dst, s.h_pC + src, (size_t)n * 4);
     if (counts) counts[d] = n;
   }
   return 0;
@@ -218,7 +238,7 @@ int Ingest::finish(Slot& s, const int64_t* doc_off, float* ent, float* nrm, floa
 
 int Ingest::run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, float* ent,
                 float* nrm, float* coh, float* emb, int32_t* starts, int32_t* lens,
-                int32_t* counts) {
+                int32_t* counts, const PatchOut& pm) {
   if (emb && !cfg.with_embeddings)
     return fail(BLT_ERR_INVALID, "ingest_run: embeddings asked of an ingest made without them");
   const int64_t T = cfg.row_len, B = cfg.rows;
@@ -248,7 +268,7 @@ int Ingest::run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, f
   int k = 0, rc;
   while (head < pending.size()) {
     Slot& s = slot[k];
-    if ((rc = finish(s, doc_off, ent, nrm, coh, emb, starts, lens, counts))) return rc;
+    if ((rc = finish(s, doc_off, ent, nrm, coh, emb, starts, lens, counts, pm))) return rc;
     std::fill(fill.begin(), fill.end(), 0);
     s.docs.clear();
     s.out_tokens = 0;
@@ -322,6 +342,10 @@ int Ingest::run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, f
                                              cfg.mode, nullptr, s.d_starts, s.d_lens,
                                              s.d_counts, ks)))
       return rc;
+    // per-patch means (pipeline.rs:240-258) over the same per-document rows
+    if (pm.any() && (rc = launch_patch_means(s.d_H, s.d_N, s.d_C, s.d_starts, s.d_counts, nd, 0,
+                                             s.d_doff, s.d_dlen, s.d_pH, s.d_pN, s.d_pC, ks)))
+      return rc;
     BLT_HIP_CHECK(hipEventRecord(s.computed, ks));
     // ---- download ----
     BLT_HIP_CHECK(hipStreamWaitEvent(down, s.computed, 0));
@@ -335,12 +359,15 @@ int Ingest::run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, f
     BLT_HIP_CHECK(hipMemcpyAsync(s.h_lens, s.d_lens, ob, hipMemcpyDeviceToHost, down));
     BLT_HIP_CHECK(hipMemcpyAsync(s.h_counts, s.d_counts, (size_t)nd * 4, hipMemcpyDeviceToHost,
                                  down));
+    if (pm.ent) BLT_HIP_CHECK(hipMemcpyAsync(s.h_pH, s.d_pH, ob, hipMemcpyDeviceToHost, down));
+    if (pm.prom) BLT_HIP_CHECK(hipMemcpyAsync(s.h_pN, s.d_pN, ob, hipMemcpyDeviceToHost, down));
+    if (pm.coh) BLT_HIP_CHECK(hipMemcpyAsync(s.h_pC, s.d_pC, ob, hipMemcpyDeviceToHost, down));
     BLT_HIP_CHECK(hipEventRecord(s.done, down));
     s.busy = true;
     k ^= 1;
   }
   for (Slot& s : slot)
-    if ((rc = finish(s, doc_off, ent, nrm, coh, emb, starts, lens, counts))) return rc;
+    if ((rc = finish(s, doc_off, ent, nrm, coh, emb, starts, lens, counts, pm))) return rc;
   if (counts)
     for (int64_t dd = 0; dd < n_docs; ++dd)
       if (doc_off[dd + 1] == doc_off[dd]) counts[dd] = 0;
@@ -482,14 +509,28 @@ int blt_ingest_destroy(blt_ingest* g) {
 int blt_ingest_run(blt_ingest* g, const int32_t* tokens, const int64_t* doc_offsets,
                    int64_t n_docs, float* entropies, float* norms, float* coherence,
                    float* embeddings, int32_t* starts, int32_t* lengths, int32_t* counts) {
+  return blt_ingest_run_patch_means(g, tokens, doc_offsets, n_docs, entropies, norms, coherence,
+                                    embeddings, starts, lengths, counts, nullptr, nullptr,
+                                    nullptr);
+}
+
+int blt_ingest_run_patch_means(blt_ingest* g, const int32_t* tokens, const int64_t* doc_offsets,
+                               int64_t n_docs, float* entropies, float* norms, float* coherence,
+                               float* embeddings, int32_t* starts, int32_t* lengths,
+                               int32_t* counts, float* patch_entropy, float* patch_prominence,
+                               float* patch_coherence) {
   if (!g) return fail(BLT_ERR_INVALID, "ingest_run: null handle");
   if (n_docs < 0) return fail(BLT_ERR_SHAPE, "ingest_run: n_docs >= 0");
   if (n_docs == 0) return BLT_OK;
   if (!doc_offsets || (!tokens && doc_offsets[n_docs] > 0))
     return fail(BLT_ERR_INVALID, "ingest_run: null argument");
   if (doc_offsets[0] != 0) return fail(BLT_ERR_SHAPE, "ingest_run: doc_offsets[0] must be 0");
+  Ingest::PatchOut pm;
+  pm.ent = patch_entropy;
+  pm.prom = patch_prominence;
+  pm.coh = patch_coherence;
   return reinterpret_cast<Ingest*>(g)->run(tokens, doc_offsets, n_docs, entropies, norms,
-                                           coherence, embeddings, starts, lengths, counts);
+                                           coherence, embeddings, starts, lengths, counts, pm);
 }
 
 }  // extern "C"

@@ -466,6 +466,46 @@ __global__ __launch_bounds__(PB_THREADS) void patch_boundary_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Per-patch means: the mean entropy, mean prominence (pre-norm L2 norm) and
+// mean coherence of every patch (compute_mean_entropy / compute_mean_prominence,
+// pipeline.rs:240-258; the per-segment coherence of huggingface_loader.rs:
+// 265-295).  Patch p of a row covers [starts[p], starts[p + 1]), the last one
+// running to the row end; each sum runs left to right in f32 and is divided
+// by the patch length, as the reference's iter().sum::<f32>() / n does, so the
+// results are bit-identical to it.  Row layout as in patch_boundary_kernel;
+// starts and the outputs share the row offsets.  One block per row, one thread
+// per patch (patches are short; the rare long one only delays its own thread).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void patch_means_kernel(
+    const float* __restrict__ H, const float* __restrict__ N, const float* __restrict__ C,
+    const int32_t* __restrict__ starts, const int32_t* __restrict__ count, int64_t T_dense,
+    const int64_t* __restrict__ row_off, const int32_t* __restrict__ row_len,
+    float* __restrict__ mH, float* __restrict__ mN, float* __restrict__ mC) {
+  const int64_t b = blockIdx.x;
+  const int64_t roff = row_off ? row_off[b] : b * T_dense;
+  const int64_t T = row_len ? (int64_t)row_len[b] : T_dense;
+  int64_t n = count[b];
+  n = n < 0 ? 0 : (n > T ? T : n);
+  for (int64_t p = threadIdx.x; p < n; p += blockDim.x) {
+    int64_t e = p + 1 < n ? (int64_t)starts[roff + p + 1] : T;
+    e = e < 0 ? 0 : (e > T ? T : e);
+    int64_t st = starts[roff + p];
+    st = st < 0 ? 0 : (st > e ? e : st);
+    float sh = 0.f, sn = 0.f, sc = 0.f;
+    for (int64_t t = st; t < e; ++t) {
+      sh += H[roff + t];
+      sn += N[roff + t];
+      if (C) sc += C[roff + t];
+    }
+    const float len = (float)(e - st);
+    const bool any = e > st;
+    if (mH) mH[roff + p] = any ? sh / len : 0.f;
+    if (mN) mN[roff + p] = any ? sn / len : 0.f;
+    if (mC) mC[roff + p] = any ? sc / len : 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
 namespace {
@@ -730,6 +770,16 @@ int launch_patch_boundaries_varlen(const float* H, const int64_t* row_off, const
   hipLaunchKernelGGL(patch_boundary_kernel, dim3((unsigned)rows), dim3(PB_THREADS), 0, s, H,
                      (int64_t)0, thr, mode, mask, starts, lengths, count, row_off, row_len);
   BLT_LAUNCH_CHECK("patch_boundary_kernel");
+  return 0;
+}
+
+int launch_patch_means(const float* H, const float* N, const float* C, const int32_t* starts,
+                       const int32_t* count, int64_t B, int64_t T, const int64_t* row_off,
+                       const int32_t* row_len, float* mH, float* mN, float* mC, hipStream_t s) {
+  if (B == 0) return 0;
+  hipLaunchKernelGGL(patch_means_kernel, dim3((unsigned)B), dim3(256), 0, s, H, N, C, starts,
+                     count, T, row_off, row_len, mH, mN, mC);
+  BLT_LAUNCH_CHECK("patch_means_kernel");
   return 0;
 }
 

@@ -75,6 +75,10 @@ class IngestResult:
     lengths: np.ndarray       # int32 [total]
     counts: np.ndarray        # int32 [n_docs]
     embeddings: Optional[np.ndarray] = None  # f32 [total, dim]
+    # per-patch means (run(..., patch_means=True)), laid out like starts
+    patch_entropy: Optional[np.ndarray] = None
+    patch_prominence: Optional[np.ndarray] = None
+    patch_coherence: Optional[np.ndarray] = None
 
     def doc(self, d):
         """(entropies, norms, coherence, starts, lengths[, embeddings]) of document d."""
@@ -85,6 +89,16 @@ class IngestResult:
         if self.embeddings is not None:
             out.append(self.embeddings[a:b])
         return tuple(out)
+
+    def patches(self, d):
+        """Document d's patches as the reference's PatchData fields
+        (pipeline.rs:47-60): (start offsets, lengths, mean entropy, mean
+        prominence, mean coherence); the means need run(..., patch_means=True)."""
+        a, n = int(self.offsets[d]), int(self.counts[d])
+        if self.patch_entropy is None:
+            raise BltError("per-patch means were not computed (run with patch_means=True)")
+        return (self.starts[a:a + n], self.lengths[a:a + n], self.patch_entropy[a:a + n],
+                self.patch_prominence[a:a + n], self.patch_coherence[a:a + n])
 
 
 class StreamingIngest:
@@ -119,8 +133,9 @@ class StreamingIngest:
             _lib.lib().blt_ingest_destroy(h)
             self._h = None
 
-    def run(self, tokens, offsets):
-        """tokens int32 [total] (host), offsets int64 [n_docs + 1] -> IngestResult."""
+    def run(self, tokens, offsets, patch_means=False):
+        """tokens int32 [total] (host), offsets int64 [n_docs + 1] -> IngestResult
+        (with the per-patch means of every document when patch_means)."""
         tok = np.ascontiguousarray(tokens, dtype=np.int32)
         off = np.ascontiguousarray(offsets, dtype=np.int64)
         if off.ndim != 1 or off.size < 1 or off[0] != 0 or off[-1] != tok.size:
@@ -133,10 +148,15 @@ class StreamingIngest:
             lengths=np.zeros(total, np.int32), counts=np.zeros(nd, np.int32),
             embeddings=(np.zeros((total, self.model.cfg.dim), np.float32)
                         if self.with_embeddings else None))
+        if patch_means:
+            res.patch_entropy = np.zeros(total, np.float32)
+            res.patch_prominence = np.zeros(total, np.float32)
+            res.patch_coherence = np.zeros(total, np.float32)
         p = lambda a: a.ctypes.data if a is not None and a.size else None  # noqa: E731
-        check(_lib.lib().blt_ingest_run(
+        check(_lib.lib().blt_ingest_run_patch_means(
             self._h, p(tok), off.ctypes.data, nd, p(res.entropies), p(res.norms),
-            p(res.coherence), p(res.embeddings), p(res.starts), p(res.lengths), p(res.counts)),
+            p(res.coherence), p(res.embeddings), p(res.starts), p(res.lengths), p(res.counts),
+            p(res.patch_entropy), p(res.patch_prominence), p(res.patch_coherence)),
             "blt_ingest_run")
         return res
 

@@ -109,6 +109,22 @@ class LMTransformer:
               "blt_model_create")
         self._h = h
 
+    @classmethod
+    def from_safetensors(cls, path, cfg=None, device=0, max_tokens=None, window=0):
+        """load_entropy_model (model_loader.rs:103-145) from a local safetensors
+        checkpoint with facebook/blt-entropy tensor names: the config defaults to
+        entropy_model_config() and the FFN width comes from the file."""
+        from .safetensors_io import load_entropy_weights
+        w, shp = load_entropy_weights(path)
+        cfg = cfg or entropy_model_config()
+        if (cfg.dim, cfg.n_layers, cfg.vocab_size) != (shp["dim"], shp["n_layers"], shp["vocab"]):
+            raise BltError("checkpoint %s holds dim %d, %d layers, vocab %d; the config says "
+                           "dim %d, %d layers, vocab %d" % (path, shp["dim"], shp["n_layers"],
+                                                            shp["vocab"], cfg.dim, cfg.n_layers,
+                                                            cfg.vocab_size))
+        return cls(cfg, w, device=device, max_tokens=max_tokens, window=window,
+                   hidden=shp["hidden"])
+
     def __del__(self):
         h = getattr(self, "_h", None)
         # at interpreter exit the module globals may already be gone

@@ -13,7 +13,8 @@ from .fused_ops import fused_entropy
 
 __all__ = ["entropy", "patch_start_mask_from_entropy_with_monotonicity",
            "patch_start_mask_global", "patch_boundaries", "patch_start_indices_cpu",
-           "patch_lengths_from_start_indices", "PATCH_MONOTONIC", "PATCH_GLOBAL"]
+           "patch_lengths_from_start_indices", "patch_means", "PATCH_MONOTONIC",
+           "PATCH_GLOBAL"]
 
 
 def entropy(scores):
@@ -77,3 +78,42 @@ def patch_lengths_from_start_indices(start_indices, seq_len):
         out.append([(idx[i + 1] if i + 1 < len(idx) else seq_len) - idx[i]
                     for i in range(len(idx))])
     return out
+
+
+def patch_means(entropies, norms, starts, counts, coherence=None, out=None):
+    """Per-patch means on the device (compute_mean_entropy /
+    compute_mean_prominence, pipeline.rs:240-258; segment coherence,
+    huggingface_loader.rs:265-295): for patch p of row b (starts / counts as
+    patch_boundaries returns them) the left-to-right f32 mean of entropies,
+    norms and (optionally) coherence over [starts[b, p], next start or seq).
+    Returns (mean_entropy, mean_prominence, mean_coherence or None), each
+    [B, T] f32 with counts[b] valid entries per row."""
+    for t in (entropies, norms, starts, counts):
+        require_cuda(t)
+    H = contiguous(entropies.to(torch.float32))
+    N = contiguous(norms.to(torch.float32))
+    if H.dim() != 2 or N.shape != H.shape:
+        raise BltError("patch_means expects entropies and norms [batch, seq]")
+    B, T = H.shape
+    st = contiguous(starts.to(torch.int32))
+    ct = contiguous(counts.to(torch.int32))
+    if tuple(st.shape) != (B, T) or tuple(ct.shape) != (B,):
+        raise BltError("patch_means expects starts [batch, seq] and counts [batch]")
+    C = None
+    if coherence is not None:
+        require_cuda(coherence)
+        C = contiguous(coherence.to(torch.float32))
+        if C.shape != H.shape:
+            raise BltError("patch_means: coherence must match entropies")
+    if out is not None:
+        mH, mN, mC = out
+    else:
+        mH = torch.empty((B, T), dtype=torch.float32, device=H.device)
+        mN = torch.empty((B, T), dtype=torch.float32, device=H.device)
+        mC = torch.empty((B, T), dtype=torch.float32, device=H.device) if C is not None else None
+    check(_lib.lib().blt_patch_means(H.data_ptr(), N.data_ptr(),
+                                     C.data_ptr() if C is not None else None, st.data_ptr(),
+                                     ct.data_ptr(), B, T, mH.data_ptr(), mN.data_ptr(),
+                                     mC.data_ptr() if mC is not None else None,
+                                     stream_ptr(H.device)), "patch_means")
+    return mH, mN, mC

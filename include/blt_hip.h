@@ -140,6 +140,21 @@ int blt_patch_boundaries(const float* H, int64_t B, int64_t T, float thr, int32_
                          int32_t* mask, int32_t* starts, int32_t* lengths, int32_t* count,
                          blt_stream_t stream);
 
+/* Per-patch means over the patches blt_patch_boundaries found: for row b and
+ * patch p < count[b], the patch covers [starts[b*T + p], starts[b*T + p + 1]) (the
+ * last to T) and
+ *   mean_entropy[b*T + p]    = sum(entropies) / length   (compute_mean_entropy)
+ *   mean_prominence[b*T + p] = sum(norms) / length       (compute_mean_prominence)
+ *   mean_coherence[b*T + p]  = sum(coherence) / length   (segment coherence)
+ * with left-to-right f32 sums, as pipeline.rs:240-258 and huggingface_loader.rs:
+ * 265-295 compute them; an empty patch gives 0.  entropies / norms / coherence
+ * [B, T] f32; starts [B, T], count [B] int32 as blt_patch_boundaries writes them.
+ * coherence and mean_coherence may both be NULL; any output may be NULL. */
+int blt_patch_means(const float* entropies, const float* norms, const float* coherence,
+                    const int32_t* starts, const int32_t* count, int64_t B, int64_t T,
+                    float* mean_entropy, float* mean_prominence, float* mean_coherence,
+                    blt_stream_t stream);
+
 /* Entropy model: LMTransformer (src/model.rs) ------------------------- */
 
 /* LMTransformerConfig (model.rs:167-180) with the derived sizes resolved. */
@@ -297,6 +312,16 @@ int blt_ingest_destroy(blt_ingest* g);
 int blt_ingest_run(blt_ingest* g, const int32_t* tokens, const int64_t* doc_offsets,
                    int64_t n_docs, float* entropies, float* norms, float* coherence,
                    float* embeddings, int32_t* starts, int32_t* lengths, int32_t* counts);
+/* blt_ingest_run that also writes the per-patch means of every document
+ * (PatchData.entropy / .prominence, pipeline.rs:47-60 and 240-258; segment
+ * coherence, huggingface_loader.rs:265-295): patch_entropy / patch_prominence /
+ * patch_coherence [total] host f32, document d's patches at doc_offsets[d] ..
+ * + counts[d] like starts.  Any of them may be null. */
+int blt_ingest_run_patch_means(blt_ingest* g, const int32_t* tokens, const int64_t* doc_offsets,
+                               int64_t n_docs, float* entropies, float* norms, float* coherence,
+                               float* embeddings, int32_t* starts, int32_t* lengths,
+                               int32_t* counts, float* patch_entropy, float* patch_prominence,
+                               float* patch_coherence);
 /* Counts of the last blt_ingest_run: non-empty documents and their tokens,
  * tokens run through the model (chunks, overlap context included) and
  * packed-row slots launched (batches * rows * row_len, padding included). */

@@ -56,13 +56,16 @@ def lib():
         L.oracle_patch_indices.argtypes = [_i32p, _i64, _i64, _i32p, _i32p]
         L.oracle_patch_lengths.argtypes = [_i32p, _i32p, _i64, _i64, _i32p]
         L.oracle_rope_table.argtypes = [_f32p, _i32, _i32, ctypes.c_double]
+        L.oracle_patch_means.argtypes = [_f32p, _f32p, _f32p, _i32p, _i32p, _i64, _i64, _f32p,
+                                         _f32p, _f32p]
         L.oracle_attention.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i32, _i32,
                                        _i32, ctypes.c_double]
         L.oracle_model_forward.argtypes = [ctypes.POINTER(Cfg), ctypes.POINTER(Weights), _i32p,
                                            _i64, _i64, _f32p, _f32p, _f32p, _f32p, _f32p]
         for f in ("oracle_entropy", "oracle_rms_norm", "oracle_l2_norm", "oracle_softmax",
                   "oracle_silu_gate", "oracle_coherence", "oracle_patch_mask",
-                  "oracle_patch_indices", "oracle_patch_lengths", "oracle_rope_table",
+                  "oracle_patch_indices", "oracle_patch_lengths", "oracle_patch_means",
+                  "oracle_rope_table",
                   "oracle_attention", "oracle_model_forward"):
             getattr(L, f).restype = None
         _lib = L
@@ -160,6 +163,28 @@ def patch_lengths(starts, seq_len):
     lib().oracle_patch_lengths(st.ctypes.data_as(_i32p), counts.ctypes.data_as(_i32p), B, seq_len,
                                ln.ctypes.data_as(_i32p))
     return [ln[b, :counts[b]].tolist() for b in range(B)]
+
+
+def patch_means(H, norms, starts, counts, coherence=None):
+    """Per-patch means (pipeline.rs:240-258): H / norms / coherence [B, T] f32,
+    starts [B, T] int32 (count[b] valid per row) -> (mean_H, mean_norm,
+    mean_coherence or None), each [B, T] with count[b] valid entries per row."""
+    H, pH = _f(H)
+    N, pN = _f(norms)
+    B, T = H.shape
+    st, ps = _i(starts)
+    ct, pc = _i(counts)
+    mH = np.zeros((B, T), np.float32)
+    mN = np.zeros((B, T), np.float32)
+    if coherence is not None:
+        C, pC = _f(coherence)
+        mC = np.zeros((B, T), np.float32)
+        pmC = mC.ctypes.data_as(_f32p)
+    else:
+        C, pC, mC, pmC = None, None, None, None
+    lib().oracle_patch_means(pH, pN, pC, ps, pc, B, T, mH.ctypes.data_as(_f32p),
+                             mN.ctypes.data_as(_f32p), pmC)
+    return mH, mN, mC
 
 
 def rope_table(head_dim, max_seqlen, theta):

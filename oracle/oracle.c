@@ -17,7 +17,9 @@
  *   oracle_rms_norm       fp64 numpy of model.rs:758-770 / rms_norm_kernel.rs
  *   oracle_l2_norm, oracle_softmax, oracle_silu_gate, oracle_coherence
  *                         fp64 numpy + invariants (rows sum to 1, [0,1])
- *   oracle_patch_*        hand-built vectors + brute force (bit-exact)
+ *   oracle_patch_*        hand-built vectors + brute force (bit-exact);
+ *                         patch_means also: sum(mean * length) = row sum,
+ *                         constant rows -> the constant, numpy fsum / length
  *   oracle_rope_table     fp64 closed form, identity at pos 0
  *   oracle_attention      fp64 numpy with a materialised mask; row 0 = v[0];
  *                         window >= T equals full causal
@@ -146,6 +148,32 @@ EXPORT void oracle_patch_lengths(const int32_t* starts, const int32_t* counts, i
       const int32_t s = starts[b * T + i];
       const int32_t e = i + 1 < counts[b] ? starts[b * T + i + 1] : (int32_t)T;
       lengths[b * T + i] = e - s;
+    }
+}
+
+/* ---- pipeline.rs:240-258 — compute_mean_entropy / compute_mean_prominence:
+ * sum of the patch's values, left to right in f32, over its length (0 for an
+ * empty range); huggingface_loader.rs:265-295 averages coherence the same way.
+ * Patch i of row b covers [starts[b*T + i], next start or T).  C / mC may be NULL. */
+EXPORT void oracle_patch_means(const float* H, const float* N, const float* C,
+                               const int32_t* starts, const int32_t* counts, int64_t B,
+                               int64_t T, float* mH, float* mN, float* mC) {
+  for (int64_t b = 0; b < B; ++b)
+    for (int32_t i = 0; i < counts[b]; ++i) {
+      int64_t e = i + 1 < counts[b] ? starts[b * T + i + 1] : T;
+      if (e > T) e = T;
+      int64_t s = starts[b * T + i];
+      if (s > e) s = e;
+      float sh = 0.0f, sn = 0.0f, sc = 0.0f;
+      for (int64_t t = s; t < e; ++t) {
+        sh += H[b * T + t];
+        sn += N[b * T + t];
+        if (C) sc += C[b * T + t];
+      }
+      const float len = (float)(e - s);
+      mH[b * T + i] = e > s ? sh / len : 0.0f;
+      mN[b * T + i] = e > s ? sn / len : 0.0f;
+      if (mC) mC[b * T + i] = e > s ? sc / len : 0.0f;
     }
 }
 

@@ -217,3 +217,35 @@ def test_ingest_rejects_bad_shapes():
         ing.run(toks, off)
     res = ing.run(*_docs(8, [10, 20]))  # the handle still works after the error
     assert res.counts.size == 2 and int(res.lengths[:res.counts[0]].sum()) == 10
+
+
+def test_ingest_patch_means_bit_exact():
+    """Per-patch means of every document (PatchData.entropy / .prominence,
+    pipeline.rs:240-258) from the ingest driver equal the oracle's restatement
+    applied to that document's own stitched entropies, norms and starts."""
+    cfg = M.LMTransformerConfig(**TINY)
+    w = M.random_weights(cfg, 29, hidden=256)
+    m = M.LMTransformer(cfg, w, device=0, max_tokens=4 * 128, window=0)
+    conf = I.BltConfig(threshold=0.3, max_seq_len=64, chunk_overlap=16)
+    ing = I.StreamingIngest(m, conf, rows=4, row_len=128)
+    lens = [0, 1, 3, 40, 64, 65, 200, 7, 0, 128]
+    toks, off = _docs(synth.config_seed(5) + 11, lens)
+    res = ing.run(toks, off, patch_means=True)
+    plain = ing.run(toks, off)
+    assert np.array_equal(plain.starts, res.starts) and np.array_equal(plain.entropies,
+                                                                        res.entropies)
+    for d, L in enumerate(lens):
+        H, N, C, S, Lp = res.doc(d)
+        starts, lengths, pH, pN, pC = res.patches(d)
+        assert np.array_equal(starts, S) and int(Lp.sum()) == L
+        if L == 0:
+            assert pH.size == 0
+            continue
+        n = S.size
+        st = np.zeros((1, L), np.int32)
+        st[0, :n] = S
+        rH, rN, rC = oracle.patch_means(H[None], N[None], st, np.array([n], np.int32), C[None])
+        assert np.array_equal(pH, rH[0, :n]) and np.array_equal(pN, rN[0, :n])
+        assert np.array_equal(pC, rC[0, :n])
+    with pytest.raises(BltError):
+        plain.patches(3)

@@ -102,3 +102,26 @@ def test_full_size_properties():
     ln = lengths.cpu()
     for b in range(B):
         assert int(ln[b, :c[b]].sum()) == T
+
+
+def test_from_safetensors_matches_in_memory_weights(tmp_path):
+    """A facebook/blt-entropy style checkpoint (PyTorch [out, in] layout) loads
+    to the same model: outputs are bit-identical to the in-memory weights, and
+    the FFN width comes from the file (model_loader.rs:103-145)."""
+    from blt_burn_amd import safetensors_io as st
+    cfg = M.LMTransformerConfig(dim=128, n_layers=2, n_heads=2, ffn_dim_multiplier=1.0,
+                                multiple_of=64, max_seqlen=256, vocab_size=260)
+    w = M.random_weights(cfg, 11, hidden=384)  # the config rule alone would give 128
+    path = str(tmp_path / "model.safetensors")
+    st.save_entropy_weights(path, w)
+    tok = torch.from_numpy(synth.tokens(synth.config_seed(4), (2, 100))).cuda()
+    a = M.LMTransformer(cfg, w, device=0, max_tokens=200).forward_with_embeddings(tok)
+    mb = M.LMTransformer.from_safetensors(path, cfg, device=0, max_tokens=200)
+    assert mb.hidden == 384
+    b = mb.forward_with_embeddings(tok)
+    torch.cuda.synchronize()
+    for n in ("logits", "pre_norm_embeddings", "embedding_norms", "entropies"):
+        assert torch.equal(getattr(a, n), getattr(b, n)), n
+    bad = M.LMTransformerConfig(dim=128, n_layers=3, n_heads=2, max_seqlen=256)
+    with pytest.raises(M.BltError):
+        M.LMTransformer.from_safetensors(path, bad, device=0, max_tokens=200)
