@@ -135,8 +135,11 @@ def summarize_trace(path):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--config", type=int, default=4, choices=(4, 5),
+    ap.add_argument("--config", type=int, default=4, choices=(1, 2, 3, 4, 5),
                     help="4: [16, 8192] forward + boundaries (the headline metric); "
+                         "1: fused entropy + patch boundaries over f32 logits [4, 8192, 260]; "
+                         "2: RMSNorm + pre-norm L2 [32768, 768] and SiLU*gate [32768, 2048], "
+                         "bf16; 3: causal RoPE attention B=8 T=4096 H=12 d=64 W=512; "
                          "5: streaming ingest of variable-length documents, end to end")
     ap.add_argument("--steps", type=int, default=None,
                     help="timed steps (config 4: batches, default 10; config 5: passes over "
@@ -197,6 +200,9 @@ def main():
         sys.exit(1)
     if args.config == 5:
         bench_ingest(args)
+        return
+    if args.config in (1, 2, 3):
+        (bench_config1, bench_config2, bench_config3)[args.config - 1](args)
         return
     if args.steps is None:
         args.steps = 10
@@ -306,6 +312,245 @@ def main():
                 "norm_max_rel": float((np.abs(ng - ref["embedding_norms"])
                                        / ref["embedding_norms"]).max())},
         }
+    print(json.dumps(result), flush=True)
+
+
+def _timed(fn, steps, warmup):
+    """Mean ms of fn() over `steps` calls, bracketed by HIP events on the current
+    stream (the stream the library launches on)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def _cpu_cores():
+    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    os.environ["OMP_NUM_THREADS"] = str(cores)
+    return cores
+
+
+def bench_config1(args):
+    """Config 1: fused entropy over f32 logits [4, 8192, 260] ~ N(0, 2) and the
+    patch-boundary passes (global H > 1.33, monotonic dH > 0.2), inputs in HBM.
+    value = positions per second for the whole step (entropy + both passes);
+    roofline = the entropy kernel's HBM rate (1040 B read + 4 B written per
+    position) against 8 TB/s."""
+    import numpy as np
+    import torch
+    from blt_burn_amd import fused_ops, patcher, synth
+    steps = args.steps or 50
+    B, T, V = 4, 8192, 260
+    logits_np = synth.normal_f32(synth.config_seed(1), (B, T, V), 0.0, 2.0)
+    logits = torch.from_numpy(logits_np).cuda()
+    bnd = [tuple(torch.empty(s, dtype=torch.int32, device="cuda")
+                 for s in ((B, T), (B, T), (B, T), (B,))) for _ in range(2)]
+    Hbuf = {}
+
+    def step():
+        H = fused_ops.fused_entropy(logits, V)
+        Hbuf["H"] = H
+        patcher.patch_boundaries(H, 1.33, patcher.PATCH_GLOBAL, out=bnd[0])
+        patcher.patch_boundaries(H, 0.2, patcher.PATCH_MONOTONIC, out=bnd[1])
+
+    ms = _timed(step, steps, args.warmup)
+    ms_ent = _timed(lambda: fused_ops.fused_entropy(logits, V), steps, args.warmup)
+    ms_bnd = _timed(lambda: patcher.patch_boundaries(Hbuf["H"], 0.2, patcher.PATCH_MONOTONIC,
+                                                     out=bnd[1]), steps, args.warmup)
+    n = B * T
+    ent_bytes = n * (V * 4 + 4)
+    gbs = ent_bytes / (ms_ent * 1e-3) / 1e9
+    result = {
+        "metric": "positions/sec through fused entropy + global and monotonic patch boundaries "
+                  "(config 1, f32 logits [4, 8192, 260])",
+        "value": round(n / (ms * 1e-3), 1), "unit": "positions/s", "n_gpus": 1, "steps": steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: logits ~ N(0, 2.0), seed %d" % synth.config_seed(1),
+        "config": {"workload": "config1: fused_entropy + patch boundaries (global 1.33, "
+                               "monotonic 0.2)", "batch": B, "seq_len": T, "vocab": V},
+        "roofline": {"bound": "hbm", "kernel": "entropy_kernel", "achieved": round(gbs, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": None, "launch_ms": round(ms_ent, 4),
+                     "bytes_per_launch": ent_bytes},
+        "boundary_pass_ms": round(ms_bnd, 4),
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        import oracle
+        cores = _cpu_cores()
+        Bs = B
+        c0 = time.perf_counter()
+        reps = 0
+        while True:
+            Hc = oracle.entropy(logits_np[:Bs])
+            oracle.patch_mask(Hc, 1.33, 1)
+            oracle.patch_mask(Hc, 0.2, 0)
+            reps += 1
+            c1 = time.perf_counter()
+            if c1 - c0 > 2.0:
+                break
+        Hg = Hbuf["H"].cpu().numpy()[:Bs]
+        m_g = bnd[1][0].cpu().numpy()[:Bs]
+        result["cpu_baseline"] = {
+            "value": round(reps * Bs * T / (c1 - c0), 1), "unit": "positions/s",
+            "cores": cores, "kind": "port",
+            "sample": "the whole [4, 8192, 260] input through the C oracle's entropy (OpenMP) "
+                      "and both masks, %d passes in %.2f s" % (reps, c1 - c0),
+            "parity_on_sample": {"entropy_max_abs": float(np.abs(Hg - Hc).max()),
+                                 "monotonic_mask_equal": bool(
+                                     (m_g == oracle.patch_mask(Hg, 0.2, 0)).all())}}
+    print(json.dumps(result), flush=True)
+
+
+def bench_config2(args):
+    """Config 2: RMSNorm (eps 1e-5 after the root) with the pre-norm L2 norms over
+    bf16 x [32768, 768], and SiLU(a) * b over bf16 [32768, 2048].  Both are
+    HBM-bound: RMSNorm+L2 moves 1536 + 1536 + 4 B per row, SiLU*gate 6 B per
+    element.  value = rows per second through both ops; roofline = each
+    kernel's HBM rate against 8 TB/s (the slower of the two as `roofline`)."""
+    import numpy as np
+    import torch
+    from blt_burn_amd import fused_ops, synth
+    steps = args.steps or 50
+    R, D, F = 32768, 768, 2048
+    seed = synth.config_seed(2)
+    x = torch.from_numpy(synth.normal_f32(seed, (1, R, D))).cuda().to(torch.bfloat16)
+    w = torch.from_numpy(synth.normal_f32(seed + 1, (D,), 1.0, 0.02)).cuda().to(torch.bfloat16)
+    a = torch.from_numpy(synth.normal_f32(seed + 2, (R, F))).cuda().to(torch.bfloat16)
+    b = torch.from_numpy(synth.normal_f32(seed + 3, (R, F))).cuda().to(torch.bfloat16)
+    l2 = torch.empty((1, R), dtype=torch.float32, device="cuda")
+    keep = {}
+
+    def rms():
+        keep["y"] = fused_ops.fused_rms_norm(x, w, 1e-5, l2_out=l2)
+
+    def silu():
+        keep["s"] = fused_ops.fused_silu_gate(a, b)
+
+    ms_rms = _timed(rms, steps, args.warmup)
+    ms_silu = _timed(silu, steps, args.warmup)
+    rms_bytes = R * (2 * D * 2 + 4) + D * 2
+    silu_bytes = R * F * 6
+    g_rms = rms_bytes / (ms_rms * 1e-3) / 1e9
+    g_silu = silu_bytes / (ms_silu * 1e-3) / 1e9
+    worst = ("rmsnorm_kernel", g_rms, ms_rms, rms_bytes) if g_rms < g_silu else \
+        ("silu_gate_bf16_kernel", g_silu, ms_silu, silu_bytes)
+    result = {
+        "metric": "rows/sec through RMSNorm+L2 [., 768] and SiLU*gate [., 2048] (config 2, bf16)",
+        "value": round(R / ((ms_rms + ms_silu) * 1e-3), 1), "unit": "rows/s", "n_gpus": 1,
+        "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms_rms + ms_silu, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: x, a, b ~ N(0, 1), w ~ 1 + N(0, 0.02), seed %d" % seed,
+        "config": {"workload": "config2: fused_rms_norm (+pre-norm L2) and fused_silu_gate",
+                   "rows": R, "dim": D, "ffn": F, "eps": 1e-5},
+        "roofline": {"bound": "hbm", "kernel": worst[0], "achieved": round(worst[1], 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(worst[1] / PEAK_HBM_GBS, 4), "traffic": None,
+                     "launch_ms": round(worst[2], 4), "bytes_per_launch": worst[3]},
+        "kernels": {"rmsnorm_l2": {"ms": round(ms_rms, 4), "GB/s": round(g_rms, 1),
+                                   "frac": round(g_rms / PEAK_HBM_GBS, 4)},
+                    "silu_gate": {"ms": round(ms_silu, 4), "GB/s": round(g_silu, 1),
+                                  "frac": round(g_silu / PEAK_HBM_GBS, 4)}},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        import oracle
+        cores = _cpu_cores()
+        n = 4096
+        xs = x[0, :n].float().cpu().numpy()
+        ws = w.float().cpu().numpy()
+        as_, bs = a[:n].float().cpu().numpy(), b[:n].float().cpu().numpy()
+        c0 = time.perf_counter()
+        reps = 0
+        while True:
+            yr = oracle.rms_norm(xs, ws, 1e-5, 0)
+            lr = oracle.l2_norm(xs)
+            sr = oracle.silu_gate(as_, bs)
+            reps += 1
+            c1 = time.perf_counter()
+            if c1 - c0 > 2.0:
+                break
+        yg = keep["y"][0, :n].float().cpu().numpy()
+        sg = keep["s"][:n].float().cpu().numpy()
+        result["cpu_baseline"] = {
+            "value": round(reps * n / (c1 - c0), 1), "unit": "rows/s", "cores": cores,
+            "kind": "port",
+            "sample": "first %d rows through the C oracle's rms_norm, l2_norm and silu_gate "
+                      "(f32, OpenMP), %d passes in %.2f s" % (n, reps, c1 - c0),
+            "parity_on_sample": {
+                "rmsnorm_max_abs": float(np.abs(yg - yr).max()),
+                "l2_max_rel": float((np.abs(l2[0, :n].cpu().numpy() - lr) / lr).max()),
+                "silu_gate_max_abs": float(np.abs(sg - sr).max())}}
+    print(json.dumps(result), flush=True)
+
+
+def bench_config3(args):
+    """Config 3: causal attention with RoPE (theta 10000, half-split) and a
+    512-key window, bf16 q, k, v [8, 12, 4096, 64] ~ N(0, 1), f32 softmax.
+    value = visible (query, key) pairs per second; roofline = 4 d = 256 FLOP
+    per visible pair over the fused call (RoPE pre-pass + attention kernel)
+    against 2.5 PFLOP/s bf16; the attention kernel alone is reported beside it."""
+    import numpy as np
+    import torch
+    from blt_burn_amd import fused_ops, synth
+    steps = args.steps or 20
+    B, H, T, d, W = 8, 12, 4096, 64, 512
+    seed = synth.config_seed(3)
+    qkv = [torch.from_numpy(synth.normal_f32(seed + i, (B, H, T, d))).cuda().to(torch.bfloat16)
+           for i in range(3)]
+    keep = {}
+
+    def run_rope():
+        keep["o"] = fused_ops.fused_attention(*qkv, True, window=W, rope_theta=10000.0)
+
+    def run_plain():
+        fused_ops.fused_attention(*qkv, True, window=W, rope_theta=0.0)
+
+    ms = _timed(run_rope, steps, args.warmup)
+    ms_attn = _timed(run_plain, steps, args.warmup)
+    pairs = attention_pairs(T, W) * B * H
+    flops = 4.0 * d * pairs
+    tf = flops / (ms * 1e-3) / 1e12
+    tf_attn = flops / (ms_attn * 1e-3) / 1e12
+    result = {
+        "metric": "visible (query, key) pairs/sec of causal RoPE attention, window 512 "
+                  "(config 3, bf16)",
+        "value": round(pairs / (ms * 1e-3), 1), "unit": "pairs/s", "n_gpus": 1, "steps": steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: q, k, v ~ N(0, 1), seed %d" % seed,
+        "config": {"workload": "config3: fused_attention causal, RoPE theta 10000, window 512",
+                   "batch": B, "heads": H, "seq_len": T, "head_dim": d, "window": W},
+        "roofline": {"bound": "mfma", "kernel": "rope pre-pass + attn_fwd_kernel",
+                     "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "launch_ms": round(ms, 4), "flop_per_launch": flops},
+        "attention_kernel_only": {"ms": round(ms_attn, 4), "TFLOP/s": round(tf_attn, 2),
+                                  "frac": round(tf_attn / PEAK_BF16_TFLOPS, 4)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        import oracle
+        cores = _cpu_cores()
+        q, k, v = (t[:1].float().cpu().numpy() for t in qkv)
+        c0 = time.perf_counter()
+        ref = oracle.attention(q, k, v, True, W, 10000.0)
+        c1 = time.perf_counter()
+        got = keep["o"][:1].float().cpu().numpy()
+        result["cpu_baseline"] = {
+            "value": round(attention_pairs(T, W) * H / (c1 - c0), 1), "unit": "pairs/s",
+            "cores": cores, "kind": "port",
+            "sample": "batch row 0 (12 heads x 4096) through the C oracle's fp32 attention "
+                      "(RoPE, window 512, OpenMP), %.2f s" % (c1 - c0),
+            "parity_on_sample": {"max_abs": float(np.abs(got - ref).max())}}
     print(json.dumps(result), flush=True)
 
 

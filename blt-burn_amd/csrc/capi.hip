@@ -4,8 +4,11 @@
 #include <string.h>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <string>
 #include <thread>
+#include <tuple>
 #include <vector>
 
 #include "model.hpp"
@@ -198,6 +201,44 @@ int64_t blt_attention_workspace_bytes(int64_t B, int64_t H, int64_t T, int32_t d
   return 2 * B * H * T * d * 2 + T * d * 4 + 256;
 }
 
+// RoPE tables of the fused attention entry, one per (device, head_dim, theta):
+// built on the host in the reference's f32 order (so every value equals the
+// reference table) and uploaded once; a longer sequence rebuilds it at the
+// new length.  Tables live until the process ends.
+namespace {
+struct RopeCache {
+  std::mutex mu;
+  struct Entry {
+    float* ptr = nullptr;
+    int64_t len = 0;
+  };
+  std::map<std::tuple<int, int, uint32_t>, Entry> tables;
+} g_rope;
+}  // namespace
+
+static int rope_table_device(int d, int64_t T, float theta, const float** out) {
+  int dev = 0;
+  BLT_HIP_CHECK(hipGetDevice(&dev));
+  uint32_t tbits;
+  memcpy(&tbits, &theta, 4);
+  std::lock_guard<std::mutex> lock(g_rope.mu);
+  RopeCache::Entry& e = g_rope.tables[std::make_tuple(dev, d, tbits)];
+  if (e.len < T) {
+    std::vector<float> host((size_t)T * d);
+    rope_table_host(host.data(), d, (int)T, theta);
+    float* p = nullptr;
+    BLT_HIP_CHECK(hipMalloc((void**)&p, host.size() * 4));
+    // synchronous: the table is complete before any launch can read it
+    BLT_HIP_CHECK(hipMemcpy(p, host.data(), host.size() * 4, hipMemcpyHostToDevice));
+    // kernels queued earlier may still read the old table; hipFree waits for them
+    if (e.ptr) BLT_HIP_CHECK(hipFree(e.ptr));
+    e.ptr = p;
+    e.len = T;
+  }
+  *out = e.ptr;
+  return 0;
+}
+
 int blt_fused_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                              uint16_t* o, int64_t B, int64_t H, int64_t T, int32_t d,
                              int64_t sb_q, int64_t sh_q, int64_t st_q, int64_t sb_kv,
@@ -228,14 +269,11 @@ int blt_fused_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_
       return fail(BLT_ERR_INVALID, "fused_attention: rope needs a workspace");
     uint16_t* qr = reinterpret_cast<uint16_t*>(workspace);
     uint16_t* kr = qr + B * H * T * d;
-    float* cs = reinterpret_cast<float*>(kr + B * H * T * d);
-    std::vector<float> host((size_t)T * d);
-    rope_table_host(host.data(), d, (int)T, rope_theta);
-    BLT_HIP_CHECK(hipMemcpyAsync(cs, host.data(), host.size() * 4, hipMemcpyHostToDevice, s));
+    const float* cs = nullptr;
     int rc;
+    if ((rc = rope_table_device(d, T, rope_theta, &cs))) return rc;
     if ((rc = launch_rope(q, qr, cs, B, H, T, d, sb_q, sh_q, st_q, s))) return rc;
     if ((rc = launch_rope(k, kr, cs, B, H, T, d, sb_kv, sh_kv, st_kv, s))) return rc;
-    BLT_HIP_CHECK(hipStreamSynchronize(s));  // the host table must outlive its copy
     a.q = qr; a.sb_q = H * T * d; a.sh_q = T * d; a.st_q = d;
     a.k = kr; a.sb_k = H * T * d; a.sh_k = T * d; a.st_k = d;
   }

@@ -372,6 +372,41 @@ __global__ __launch_bounds__(256) void rope_kernel(const uint16_t* __restrict__ 
   }
 }
 
+// The same for head_dim 64 with 16-byte rows: one thread per 8 pairs, 16-byte
+// loads and stores of both halves and of the (cos, sin) table.
+__global__ __launch_bounds__(256) void rope64_kernel(const uint16_t* __restrict__ src,
+                                                     uint16_t* __restrict__ dst,
+                                                     const float* __restrict__ cs, int64_t B,
+                                                     int64_t H, int64_t T, int64_t sb,
+                                                     int64_t sh, int64_t st) {
+  constexpr int D = 64, HALF = 32, G = HALF / 8;
+  const int64_t total = B * H * T * G;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int g = (int)(i % G);
+    const int64_t r = i / G;  // (b*H + h)*T + t
+    const int64_t t = r % T;
+    const int64_t bh = r / T;
+    const int64_t h = bh % H, b = bh / H;
+    const uint16_t* s = src + b * sb + h * sh + t * st + 8 * g;
+    const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(s);
+    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(s + HALF);
+    const f32x4_t* c4 = reinterpret_cast<const f32x4_t*>(cs + (t * HALF + 8 * g) * 2);
+    uint32_t o1[4], o2[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {  // pairs 2q, 2q + 1 of this group
+      const f32x4_t c = c4[q];      // (cos, sin) of pair 2q, then of pair 2q + 1
+      const float a0 = bf16_to_f32((uint16_t)(lo[q] & 0xffff)), a1 = bf16_to_f32((uint16_t)(lo[q] >> 16));
+      const float b0 = bf16_to_f32((uint16_t)(hi[q] & 0xffff)), b1 = bf16_to_f32((uint16_t)(hi[q] >> 16));
+      o1[q] = pack_bf16x2(a0 * c.x - b0 * c.y, a1 * c.z - b1 * c.w);
+      o2[q] = pack_bf16x2(a0 * c.y + b0 * c.x, a1 * c.w + b1 * c.z);
+    }
+    uint16_t* o = dst + r * D + 8 * g;
+    *reinterpret_cast<u32x4_t*>(o) = u32x4_t{o1[0], o1[1], o1[2], o1[3]};
+    *reinterpret_cast<u32x4_t*>(o + HALF) = u32x4_t{o2[0], o2[1], o2[2], o2[3]};
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Patch boundaries: one 1024-thread block per batch row.
 //   flag[t] = 1 for t < 2; else monotonic: (H[t] - H[t-1]) > thr, global: H[t] > thr
@@ -692,6 +727,13 @@ int launch_rope(const uint16_t* src, uint16_t* dst, const float* cs, int64_t B, 
                 int64_t T, int d, int64_t sb, int64_t sh, int64_t st, hipStream_t s) {
   const int64_t total = B * H * T * (d / 2);
   if (total == 0) return 0;
+  if (d == 64 && (uintptr_t)src % 16 == 0 && (uintptr_t)dst % 16 == 0 && sb % 8 == 0 &&
+      sh % 8 == 0 && st % 8 == 0) {
+    hipLaunchKernelGGL(rope64_kernel, dim3(elementwise_grid(total / 8)), dim3(256), 0, s, src,
+                       dst, cs, B, H, T, sb, sh, st);
+    BLT_LAUNCH_CHECK("rope64_kernel");
+    return 0;
+  }
   hipLaunchKernelGGL(rope_kernel, dim3(elementwise_grid(total)), dim3(256), 0, s, src, dst, cs, B,
                      H, T, d, sb, sh, st);
   BLT_LAUNCH_CHECK("rope_kernel");
