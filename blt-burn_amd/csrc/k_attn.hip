@@ -10,7 +10,10 @@
 // (lane ^ 32) instead of a 32-lane reduction.  The output is accumulated
 // transposed, O^T = V^T . P^T, which keeps the per-query rescale factor in
 // the lane that owns the query.  The P^T registers feed the MFMA B operand
-// directly (no LDS round trip).  V stays row-major in LDS; the V^T operand is
+// directly (no LDS round trip).  The softmax is VALU-bound (a v_exp_f32 per
+// score costs about three FMA issue slots), so the row sums of P come from
+// the MFMA pipe instead: a constant all-ones A operand times P^T gives every
+// lane its query's sum of the same bf16-rounded P the numerator uses.  V stays row-major in LDS; the V^T operand is
 // read with ds_read_b64_tr_b16, whose 16-lane transpose hands each lane 4
 // consecutive keys of one head-dim column.
 //
@@ -113,16 +116,36 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
   }
 
   // K/V tile staging: thread -> (key, 16-byte chunk), two chunks each of K and V.
-  // Keys past T load key T-1 (masked: a key >= T is never visible).
+  // Each thread keeps 32-bit byte offsets of its rows; a tile adds its uniform
+  // row base, so the loads take a scalar base plus a vector offset.  In the
+  // last, partial tile keys past T load key T-1 (masked: a key >= T is never
+  // visible).
   u32x4_t rk[2], rv[2];
-  auto gload = [&](int t) {
+  uint32_t offk[2], offv[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int id2 = tid + 256 * i, key = id2 >> 3, c = id2 & 7;
-      int kk = t * BKV + key;
-      kk = kk < T ? kk : T - 1;
-      rk[i] = *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)kk * p.st_k + c * 8);
-      rv[i] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)kk * p.st_v + c * 8);
+  for (int i = 0; i < 2; ++i) {
+    const int id2 = tid + 256 * i, key = id2 >> 3, c = id2 & 7;
+    offk[i] = (uint32_t)(((int64_t)key * p.st_k + c * 8) * 2);
+    offv[i] = (uint32_t)(((int64_t)key * p.st_v + c * 8) * 2);
+  }
+  auto gload = [&](int t) {
+    const int64_t k0 = (int64_t)t * BKV;
+    const char* kb0 = reinterpret_cast<const char*>(kbase + k0 * p.st_k);
+    const char* vb0 = reinterpret_cast<const char*>(vbase + k0 * p.st_v);
+    if (k0 + BKV <= T) {  // uniform: the whole tile is in range
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        rk[i] = *reinterpret_cast<const u32x4_t*>(kb0 + offk[i]);
+        rv[i] = *reinterpret_cast<const u32x4_t*>(vb0 + offv[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int key = (tid + 256 * i) >> 3;
+        const int64_t back = k0 + key < T ? 0 : k0 + key - (T - 1);  // rows to step back
+        rk[i] = *reinterpret_cast<const u32x4_t*>(kb0 + offk[i] - back * p.st_k * 2);
+        rv[i] = *reinterpret_cast<const u32x4_t*>(vb0 + offv[i] - back * p.st_v * 2);
+      }
     }
   };
   auto sstore = [&](int stage) {
@@ -144,16 +167,22 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
   const int vt_lane = (4 * lhalf + (s16 >> 2)) * V_LD + 16 * ((lane >> 4) & 1) + 4 * (s16 & 3);
 
   f32x16_t o[NQ][2];
-  float m[NQ], l[NQ];
+  // lsum[qq][0]: running sum of P for this lane's query (every element of the
+  // accumulator holds it; only element 0 is rescaled and read)
+  f32x16_t lsum[NQ];
+  float m[NQ];
 #pragma unroll
   for (int qq = 0; qq < NQ; ++qq) {
     m[qq] = -INFINITY;
-    l[qq] = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) lsum[qq][r] = 0.f;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[qq][j][r] = 0.f;
   }
+  const bf16x8_t ones = __builtin_bit_cast(
+      bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});  // bf16 1.0
   const float sl2 = 0.125f * 1.44269504088896340736f;  // 1/sqrt(64) * log2(e)
 
   gload(t_begin);
@@ -189,29 +218,39 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
       // The running max used for exponentiation (m) only moves when a row's
       // max grows by more than 2^8 (checked wave-wide), so P <= 256 and the
       // O / l rescale is skipped for most tiles; O / l is unchanged by it.
-      const bool need_mask = (p.causal && kb + BKV - 1 > qw) ||
-                             (window > 0 && kb <= qw + QPW - 1 - window) || (kb + BKV > T) ||
-                             kb < wseg_hi;
+      // upper bound (causal diagonal, keys past T) and lower bound (window
+      // edge, segment start) are applied only in the tiles that cross them
+      const bool mask_hi = (p.causal && kb + BKV - 1 > qw) || (kb + BKV > T);
+      const bool mask_lo = (window > 0 && kb <= qw + QPW - 1 - window) || kb < wseg_hi;
       bf16x8_t pb[NQ][2][2];
 #pragma unroll
       for (int qq = 0; qq < NQ; ++qq) {
         const int qi = qw + 32 * qq + lrow;
-        if (need_mask) {
+        // element (sub, r) holds key kb + 4 * lhalf + (a compile-time offset)
+        if (mask_hi) {
           const int lim_hi = p.causal ? (qi < T - 1 ? qi : T - 1) : T - 1;  // key <= lim_hi
-          int lim_lo = window > 0 ? qi - window : -1;                        // key > lim_lo
-          if (p.causal) {
-            const int sg = seg_at(qi) - 1;
-            lim_lo = lim_lo > sg ? lim_lo : sg;
-          }
-          // element (sub, r) holds key kb + 4 * lhalf + (a compile-time offset)
-          const int hi_rel = lim_hi - kb - 4 * lhalf, lo_rel = lim_lo - kb - 4 * lhalf;
+          const int hi_rel = lim_hi - kb - 4 * lhalf;
 #pragma unroll
           for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int ko = sub * 32 + 8 * (r >> 2) + (r & 3);
-              const bool vis = (ko <= hi_rel) & (ko > lo_rel);
-              s[qq][sub][r] = vis ? s[qq][sub][r] : -INFINITY;
+              s[qq][sub][r] = ko <= hi_rel ? s[qq][sub][r] : -INFINITY;
+            }
+        }
+        if (mask_lo) {
+          int lim_lo = window > 0 ? qi - window : -1;  // key > lim_lo
+          if (p.causal) {
+            const int sg = seg_at(qi) - 1;
+            lim_lo = lim_lo > sg ? lim_lo : sg;
+          }
+          const int lo_rel = lim_lo - kb - 4 * lhalf;
+#pragma unroll
+          for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int ko = sub * 32 + 8 * (r >> 2) + (r & 3);
+              s[qq][sub][r] = ko > lo_rel ? s[qq][sub][r] : -INFINITY;
             }
         }
         float mt = -INFINITY;
@@ -224,14 +263,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
           const float m_new = fmaxf(m[qq], mt);
           const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[qq] - m_new);
           m[qq] = m_new;
-          l[qq] *= alpha;
+          lsum[qq][0] *= alpha;
 #pragma unroll
           for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) o[qq][j][r] *= alpha;
         }
         const float m_use = m[qq] == -INFINITY ? 0.f : m[qq];
-        float ls = 0.f;
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
@@ -242,12 +280,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
               const float p0 = __builtin_amdgcn_exp2f(fmaf(s[qq][sub][8 * u + e], sl2, -m_use));
               const float p1 =
                   __builtin_amdgcn_exp2f(fmaf(s[qq][sub][8 * u + e + 1], sl2, -m_use));
-              ls += p0 + p1;
               w[e >> 1] = pack_bf16x2(p0, p1);
             }
             pb[qq][sub][u] = __builtin_bit_cast(bf16x8_t, u32x4_t{w[0], w[1], w[2], w[3]});
           }
-        l[qq] += ls;
       }
       // ---- O^T += V^T . P^T ----
 #pragma unroll
@@ -267,6 +303,15 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
               o[qq][dsub] =
                   __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[qq][sub][u], o[qq][dsub], 0, 0, 0);
           }
+      // ---- row sums: lsum += ones . P^T ----
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int qq = 0; qq < NQ; ++qq)
+            lsum[qq] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, pb[qq][sub][u], lsum[qq], 0,
+                                                               0, 0);
     }
     if (t < t_end) sstore((t + 1 - t_begin) & 1);
     __syncthreads();
@@ -277,7 +322,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
   for (int qq = 0; qq < NQ; ++qq) {
     const int qi = qw + 32 * qq + lrow;
     if (qi >= T) continue;
-    const float lt = l[qq] + __shfl_xor(l[qq], 32, 64);
+    const float lt = lsum[qq][0];
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     uint16_t* orow = p.o + b * p.sb_o + h * p.sh_o + (int64_t)qi * p.st_o;
 #pragma unroll
@@ -308,6 +353,10 @@ int run_attention(const AttnArgs& a, hipStream_t s) {
 int launch_attention(const AttnArgs& a, hipStream_t s) {
   if (a.B == 0 || a.H == 0 || a.T == 0) return 0;
   if (a.T > 0x3fffffff) return fail(-2, "attention: T too large");
+  // K/V rows of a tile are addressed by 32-bit byte offsets from the tile base
+  const int64_t st = a.st_k > a.st_v ? a.st_k : a.st_v;
+  if ((st * (BKV - 1) + D) * 2 >= ((int64_t)1 << 32))
+    return fail(-2, "attention: K/V row stride too large");
   // 64 queries per wave (1 wave per SIMD) pays off for long full-causal rows;
   // with a window, 32 queries per wave (2 waves per SIMD) wastes less of
   // each masked band tile and hides latency better.
