@@ -4,6 +4,11 @@
 // store, in-place f32 residual add, RoPE on the q/k columns of the fused QKV
 // projection, SiLU*gate of the fused W1|W3 FFN).
 //
+// Two kernels share the tiling and the epilogue layout: gemm_bf16_dma_kernel
+// (global -> LDS by DMA, 256 x 256 x 64 tiles, LDS-staged epilogue; every
+// projection of the model, N % 256 == 0) and gemm_bf16_kernel (register-staged
+// loads; any N, e.g. the 260-wide head).
+//
 // Tiling: a BM x BN block tile is split over WM x WN wave64s; each wave owns a
 // (BM/WM) x (BN/WN) tile made of 32x32 v_mfma_f32_32x32x16_bf16 sub-tiles,
 // issued with the Bt fragment as the MFMA A operand so the accumulator holds
