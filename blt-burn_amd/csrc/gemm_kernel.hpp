@@ -4,10 +4,11 @@
 // store, in-place f32 residual add, RoPE on the q/k columns of the fused QKV
 // projection, SiLU*gate of the fused W1|W3 FFN).
 //
-// Two kernels share the tiling and the epilogue layout: gemm_bf16_dma_kernel
-// (global -> LDS by DMA, 256 x 256 x 64 tiles, LDS-staged epilogue; every
-// projection of the model, N % 256 == 0) and gemm_bf16_kernel (register-staged
-// loads; any N, e.g. the 260-wide head).
+// Two kernels share the tiling and the epilogue layout:
+// gemm_bf16_dma_persistent_kernel (global -> LDS by DMA, 256 x 256 x 64 tiles,
+// one persistent block per CU, LDS-staged epilogue; every projection of the
+// model, N % 256 == 0) and gemm_bf16_kernel (register-staged loads; any N,
+// e.g. the 260-wide head).
 //
 // Tiling: a BM x BN block tile is split over WM x WN wave64s; each wave owns a
 // (BM/WM) x (BN/WN) tile made of 32x32 v_mfma_f32_32x32x16_bf16 sub-tiles,
@@ -254,10 +255,9 @@ __device__ inline void epilogue(const GemmArgs& p, f32x16_t (&acc)[C::TM][C::TN]
 // fastest inside a group, so the blocks resident on one XCD share group_m A
 // row-tiles and a few Bt column-tiles in that XCD's L2 (group_m = 0: N fastest).
 template <int BM, int BN>
-__device__ inline void tile_origin(const GemmArgs& p, int64_t& m0, int64_t& n0) {
+__device__ inline void tile_origin(const GemmArgs& p, int bid, int64_t& m0, int64_t& n0) {
   const int ntm = (int)((p.M + BM - 1) / BM), ntn = (int)((p.N + BN - 1) / BN);
   const int nb = ntm * ntn;
-  const int bid = blockIdx.x;
   const int nb8 = nb & ~7;
   const int id = bid < nb8 ? (bid & 7) * (nb8 >> 3) + (bid >> 3) : bid;
   int tm, tn;
@@ -286,7 +286,7 @@ void gemm_bf16_kernel(GemmArgs p) {
   const int wm = wid / WN, wn = wid % WN;
 
   int64_t m0, n0;
-  tile_origin<BM, BN>(p, m0, n0);
+  tile_origin<BM, BN>(p, blockIdx.x, m0, n0);
 
   // Global source rows are clamped into range: rows past M (or N) load a
   // valid row whose results land in rows/columns that are never stored.
@@ -411,7 +411,17 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
     constexpr int CPR = C::WTN / 4;       // 16-byte pieces per row
     constexpr int NP = 32 * CPR / 64;     // pieces per lane per 32-row slab
     constexpr bool resid = EPI == EPI_RESID_F32;
-    float* Cf = reinterpret_cast<float*>(p.C);
+    // Rows row0 + r and columns col0 + c exist for r < mrem, c < nrem; a
+    // wave tile with none stores nothing.  Addresses are uniform bases plus
+    // 32-bit element offsets (the launcher bounds the tile's reach).
+    if (p.M <= row0 || p.N <= col0) return;
+    const int mrem = (int)(p.M - row0 < C::WTM ? p.M - row0 : C::WTM);
+    const int nrem = (int)(p.N - col0 < C::WTN ? p.N - col0 : C::WTN);
+    const int ldc = (int)p.ldc;
+    // byte addressing (uniform base + unsigned 32-bit offset) lets the
+    // loads and stores use the scalar-base addressing form
+    char* cb = reinterpret_cast<char*>(reinterpret_cast<float*>(p.C) + row0 * p.ldc + col0);
+    char* xbb = p.xb_out ? reinterpret_cast<char*>(p.xb_out + row0 * p.ldc + col0) : nullptr;
     // Residual pieces: slab i + 1's are loaded as soon as slab i's have been
     // added, so their latency overlaps slab i's stores and slab i + 1's
     // staging (one buffer: the 8-wave kernels have no registers for two).
@@ -419,11 +429,10 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
     auto load_resid = [&](int i) {
 #pragma unroll
       for (int t = 0; t < NP; ++t) {
-        const int q = lane + 64 * t, r = q / CPR, c = q % CPR;
-        int64_t row = row0 + i * 32 + r, col = col0 + c * 4;
-        row = row < p.M ? row : p.M - 1;  // out-of-range pieces are not stored
-        col = col < p.N ? col : p.N - 4;
-        res[t] = *reinterpret_cast<const f32x4_t*>(Cf + row * p.ldc + col);
+        const int q = lane + 64 * t, r = i * 32 + q / CPR, c = (q % CPR) * 4;
+        const int rr = r < mrem ? r : mrem - 1;  // out-of-range pieces are not stored
+        const int cc = c < nrem ? c : nrem - 4;
+        res[t] = *reinterpret_cast<const f32x4_t*>(cb + (unsigned)((rr * ldc + cc) * 4));
       }
     };
     if (resid) load_resid(0);
@@ -449,26 +458,25 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
       if (resid && i + 1 < C::TM) load_resid(i + 1);
 #pragma unroll
       for (int t = 0; t < NP; ++t) {
-        const int q = lane + 64 * t, r = q / CPR, c = q % CPR;
-        const int64_t row = row0 + i * 32 + r;
-        const int64_t col = col0 + c * 4;
-        const bool ok = row < p.M && col < p.N;
+        const int q = lane + 64 * t, r = i * 32 + q / CPR, c = (q % CPR) * 4;
+        const bool ok = r < mrem && c < nrem;
+        const unsigned off = (unsigned)(r * ldc + c);
         float ss = 0.f;
         if (ok) {
-          float* o = Cf + row * p.ldc + col;
+          float* o = reinterpret_cast<float*>(cb + off * 4u);
           if (resid) {
             *reinterpret_cast<f32x4_t*>(o) = v[t];
-            if (p.xb_out) {
-              *reinterpret_cast<u32x2_t*>(p.xb_out + row * p.ldc + col) =
+            if (xbb) {
+              *reinterpret_cast<u32x2_t*>(xbb + off * 2u) =
                   u32x2_t{pack_bf16x2(v[t].x, v[t].y), pack_bf16x2(v[t].z, v[t].w)};
               ss = v[t].x * v[t].x + v[t].y * v[t].y + v[t].z * v[t].z + v[t].w * v[t].w;
             }
-          } else if (col + 3 < p.n_valid && p.vec_ok) {
+          } else if (col0 + c + 3 < p.n_valid && p.vec_ok) {
             *reinterpret_cast<f32x4_t*>(o) = v[t];
           } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              if (col + e < p.n_valid) o[e] = v[t][e];
+              if (col0 + c + e < p.n_valid) o[e] = v[t][e];
           }
         }
         if (p.ss_out) {
@@ -476,7 +484,7 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
           // 64-column group of one row
           static_assert(C::WTN % 64 == 0, "norm partial sums are per 64 columns");
           ss = sum16(ss);
-          if ((c & 15) == 0 && ok) p.ss_out[row * p.ss_np + (col0 + c * 4) / 64] = ss;
+          if ((q & 15) == 0 && ok) p.ss_out[(row0 + r) * p.ss_np + (col0 + c) / 64] = ss;
         }
       }
       wave_lds_fence();
@@ -589,22 +597,6 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
   }
 }
 
-// 16 bytes per lane from global memory straight into LDS (gfx950
-// global_load_lds_dwordx4): lane i's data lands at LDS byte lds_addr + 16 * i.
-// Issued from inline asm so the compiler does not serialise it against later
-// LDS reads; the caller orders it with dma_wait_barrier.  M0 is restored.
-__device__ inline void dma16(const void* g, unsigned lds_addr) {
-  unsigned saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "global_load_lds_dwordx4 %2, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(lds_addr), "v"(g)
-      : "memory");
-}
-
 // Wait until at most N of this wave's vector-memory loads are outstanding and
 // its LDS operations are done, then barrier; the memory clobber keeps the
 // compiler from moving LDS accesses across it.
@@ -613,73 +605,103 @@ __device__ inline void dma_wait_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-// Same tiling and epilogues as gemm_bf16_kernel, but K tiles are moved
-// global -> LDS by the LDS-DMA path (no VGPR staging, no ds_write) into S LDS
-// stages, with S - 1 tiles in flight: tile kt + S - 1 is issued into the stage
-// that tile kt - 1 freed before tile kt is consumed.  Each wave issues NI
-// 1-KB DMA chunks per K tile; a chunk is RPC LDS rows of BK bf16, and lane i
-// fetches the global 16-byte piece that the swizzle places at row i / CH,
-// slot i % CH.
-template <int BM, int BN, int BK, int WM, int WN, int S, int OCC, int EPI>
-__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(OCC)))
-void gemm_bf16_dma_kernel(GemmArgs p) {
+// global_load_lds_dwordx4 with a wave-uniform 64-bit base (SGPRs) and a
+// per-lane 32-bit byte offset: lane i's 16 bytes at base + off land at LDS
+// byte lds_addr + 16 * i.  M0 is restored.
+__device__ inline void dma16_so(const void* base_in, unsigned off, unsigned lds_addr) {
+  // the base is wave-uniform by construction; make that explicit so it is
+  // held in SGPRs (readfirstlane returns int: each half goes through
+  // uint32_t so the low word is not sign-extended into the high one)
+  const uint64_t b = (uint64_t)(uintptr_t)base_in;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  const uint64_t base = (uint64_t)lo | ((uint64_t)hi << 32);
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, %3\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_addr), "v"(off), "s"(base)
+      : "memory");
+}
+
+// Same tiling and epilogues as gemm_bf16_kernel, but K tiles move global ->
+// LDS by the LDS-DMA path (no VGPR staging, no ds_write) through two LDS
+// stages, and the kernel is persistent: one block per CU walks the tiles
+// v = blockIdx.x, blockIdx.x + gridDim.x, ...  With gridDim.x a multiple of 8
+// every tile of a block has the block's XCD residue, so the tile order of
+// tile_origin holds.  The K-tile stream runs on across tiles: the next tile's
+// first K tile is issued together with the current tile's last one, so its
+// latency hides under the last MFMAs and the epilogue, and no block launch
+// sits between tiles.  Each wave issues NI 1-KB DMA chunks per K tile; a
+// chunk is RPC LDS rows of BK bf16, and lane i fetches the global 16-byte
+// piece that the swizzle places at row i / CH, slot i % CH.  LDS holds stage
+// 0 at byte 0, a gap of half a stage, then stage 1; the epilogue stages
+// through the stage that held the last K tile plus the gap, while the other
+// stage receives the next tile.  Operand rows are addressed as a per-tile
+// uniform base plus a per-lane 32-bit byte offset (the launcher checks that
+// a tile's reach fits).
+template <int BM, int BN, int BK, int WM, int WN, int EPI>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2)))
+void gemm_bf16_dma_persistent_kernel(GemmArgs p) {
   using C = GemmCfg<BM, BN, BK, WM, WN>;
   constexpr int NW = WM * WN;
   constexpr int RPC = 64 / C::CH;        // LDS rows per 1-KB chunk
   constexpr int RPB = 128 / BK;          // rows per 256 bytes (swizzle period)
   constexpr int NCH = (BM + BN) / RPC;   // 1-KB chunks per stage
-  constexpr int NI = NCH / NW;         // chunks per wave per stage
+  constexpr int NI = NCH / NW;           // chunks per wave per stage
+  constexpr int SB = C::STAGE * 2;       // bytes per stage
+  constexpr int GAP = SB / 2;
+  constexpr int SOFF = SB + GAP;         // byte offset of stage 1
   static_assert(NCH % NW == 0, "DMA chunks must divide over the waves");
-  static_assert(S >= 2, "at least two LDS stages");
-  static_assert(NW * 64 * (C::WTN + 4) * 2 <= S * C::STAGE * 2 &&
-                    NW * 32 * (C::WTN + 2) * 4 <= S * C::STAGE * 2,
-                "staged epilogue must fit in the K-loop LDS");
-  __shared__ __attribute__((aligned(1024))) uint16_t lds[S * C::STAGE];
+  static_assert((BM / RPC) % NI == 0, "a wave's chunks are all A or all Bt rows");
+  static_assert(NW * 64 * (C::WTN + 4) * 2 <= SB + GAP && NW * 32 * (C::WTN + 2) * 4 <= SB + GAP,
+                "staged epilogue must fit in a stage plus the gap");
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * SB + GAP];
 
+  const int ntiles = (int)(((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN));
+  int v = blockIdx.x;
+  if (v >= ntiles) return;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int wm = wid / WN, wn = wid % WN;
-  int64_t m0, n0;
-  tile_origin<BM, BN>(p, m0, n0);
-  const int64_t am = p.M - 1 - m0, bn = p.N - 1 - n0;
+  const int lrow = lane & 31, lhalf = lane >> 5;
   const unsigned lds_base = (unsigned)(uintptr_t)lds;
 
-  // This wave's NI chunks: per-lane source row pointers (fixed over K) and
-  // wave-uniform LDS offsets within a stage.
-  const uint16_t* gsrc[NI];
-  unsigned lofs[NI];
+  // This wave's NI chunks are all A rows or all Bt rows; chunk q covers LDS
+  // rows rb0 + q * RPC .. + RPC - 1 of that operand.
+  const bool isA = wid * NI < BM / RPC;  // uniform
+  const int rb0 = (isA ? wid * NI : wid * NI - BM / RPC) * RPC;
+  const unsigned lofs0 = (isA ? 0u : (unsigned)(BM * BK * 2)) + (unsigned)(rb0 * BK * 2);
+  const int64_t ld = isA ? p.lda : p.ldb;
+  const int64_t lim = isA ? p.M : p.N;
+  const uint16_t* opnd = isA ? p.A : p.Bt;
+  const uint16_t* gbase;  // operand row of this tile's first row (uniform)
+  unsigned goff[NI];      // byte offset of each lane's piece from gbase
+  // ln is the lane index; the tile loop passes an opaque copy after the
+  // epilogue so the offsets are recomputed there rather than held in
+  // registers across it
+  auto set_tile = [&](int64_t m0, int64_t n0, int ln) {
+    const int64_t r0 = isA ? m0 : n0;
+    const int64_t last = lim - 1 - r0;  // rows past the operand read its last row
+    gbase = opnd + r0 * ld;
 #pragma unroll
-  for (int q = 0; q < NI; ++q) {
-    const int ci = wid * NI + q;
-    const bool isA = ci < BM / RPC;  // uniform
-    const int rb = (isA ? ci : ci - BM / RPC) * RPC;
-    const int r = rb + lane / C::CH;
-    const int c = (lane % C::CH) ^ ((r / RPB) & (C::CH - 1));
-    const uint16_t* base = isA ? p.A : p.Bt;
-    const int64_t ld = isA ? p.lda : p.ldb;
-    const int64_t row = isA ? m0 + (r < am ? r : am) : n0 + (r < bn ? r : bn);
-    gsrc[q] = base + row * ld + c * 8;
-    lofs[q] = (isA ? 0u : (unsigned)(BM * BK * 2)) + (unsigned)(rb * BK * 2);
-  }
-  auto dma_tile = [&](int kt, int stage) {
-    const int64_t k0 = (int64_t)kt * BK;
-    const unsigned sbase = lds_base + (unsigned)(stage * C::STAGE * 2);
-#pragma unroll
-    for (int q = 0; q < NI; ++q)
-      dma16(gsrc[q] + k0, __builtin_amdgcn_readfirstlane(sbase + lofs[q]));
+    for (int q = 0; q < NI; ++q) {
+      const int r = rb0 + q * RPC + ln / C::CH;
+      const int c = (ln % C::CH) ^ ((r / RPB) & (C::CH - 1));
+      goff[q] = (unsigned)(((r < last ? r : last) * ld + c * 8) * 2);
+    }
   };
-
-  f32x16_t acc[C::TM][C::TN];
+  auto dma_tile = [&](int kt, int stage) {
+    const uint16_t* kb = gbase + (int64_t)kt * BK;
+    const unsigned sbase = lds_base + (unsigned)(stage * SOFF) + lofs0;
 #pragma unroll
-  for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  const int lrow = lane & 31, lhalf = lane >> 5;
+    for (int q = 0; q < NI; ++q) dma16_so(kb, goff[q], sbase + (unsigned)(q * RPC * BK * 2));
+  };
   auto load_frags = [&](int stage, int ks, bf16x8_t (&af)[C::TM], bf16x8_t (&bfr)[C::TN]) {
-    const uint16_t* sa = lds + stage * C::STAGE;
+    const uint16_t* sa = reinterpret_cast<const uint16_t*>(lds + stage * SOFF);
     const uint16_t* sb = sa + BM * BK;
     const int chunk = ks * 2 + lhalf;
 #pragma unroll
@@ -689,6 +711,7 @@ void gemm_bf16_dma_kernel(GemmArgs p) {
     for (int j = 0; j < C::TN; ++j)
       bfr[j] = *reinterpret_cast<const bf16x8_t*>(sb + swz<BK>(wn * C::WTN + j * 32 + lrow, chunk));
   };
+  f32x16_t acc[C::TM][C::TN];
   // Fragments are double-buffered: the LDS reads of K step ks + 1 are issued
   // before the MFMAs of step ks, and scheduling barriers keep the compiler
   // from sinking them back next to their uses, so each wave has LDS reads in
@@ -710,39 +733,62 @@ void gemm_bf16_dma_kernel(GemmArgs p) {
     });
   };
 
-  // Wait until tile kt's chunks have landed, allowing the `after` tiles issued
-  // later (0 .. S-2 of them) to stay in flight, then barrier.
-  auto wait_tile = [&](int after) {
-    static_for<0, S - 1>([&](auto ic) {
-      if (after == decltype(ic)::value) dma_wait_barrier<NI * decltype(ic)::value>();
-    });
-  };
   const int KT = (int)(p.K / BK);
-  const int pre = KT < S - 1 ? KT : S - 1;  // tiles issued in the prologue
-  for (int t = 0; t < pre; ++t) dma_tile(t, t);
-  // row factors, fetched under the prologue tiles' latency
+  int64_t m0, n0;
+  tile_origin<BM, BN>(p, v, m0, n0);
+  set_tile(m0, n0, lane);
+  int st = 0;  // stage of the current K tile
+  dma_tile(0, 0);
   float rs[C::TM];
   load_row_scales<C>(p, m0 + wm * C::WTM + lrow, rs);
-  wait_tile(pre - 1);
-  int st = 0;  // stage of tile kt
-  for (int kt = 0; kt < KT; ++kt) {
-    if (kt + S - 1 < KT) {
-      const int ns = st == 0 ? S - 1 : st - 1;  // stage (kt + S - 1) % S
-      dma_tile(kt + S - 1, ns);
+  dma_wait_barrier<0>();
+  for (;;) {
+    const int vn = v + (int)gridDim.x;
+    const bool more = vn < ntiles;
+    int64_t m0n = 0, n0n = 0;
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    for (int kt = 0; kt < KT; ++kt) {
+      // stage st ^ 1 was freed by the barrier that ended K tile kt - 1
+      if (kt + 1 < KT) {
+        dma_tile(kt + 1, st ^ 1);
+      } else if (more) {
+        tile_origin<BM, BN>(p, vn, m0n, n0n);
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        set_tile(m0n, n0n, ln);
+        dma_tile(0, st ^ 1);
+      }
+      compute(st);
+      if (kt + 1 < KT) dma_wait_barrier<0>();
+      st ^= 1;
     }
-    compute(st);
-    if (kt + 1 < KT) {
-      const int last = kt + S - 1 < KT - 1 ? kt + S - 1 : KT - 1;  // newest tile issued
-      wait_tile(last - (kt + 1));
-    }
-    st = st + 1 < S ? st + 1 : 0;
+    // every wave is past its last LDS read of this tile (the next tile's
+    // first K tile may still be in flight)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // an opaque lane index keeps the epilogue's per-lane addressing inside
+    // the loop (hoisted out, it would occupy registers through the K loop)
+    int le = lane;
+    asm volatile("" : "+v"(le));
+    epilogue_lds<C, EPI>(p, acc, m0, n0, wid, wm, wn, le, lds + (st == 0 ? SB : 0), rs);
+    if (!more) break;
+    v = vn;
+    m0 = m0n;
+    n0 = n0n;
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    set_tile(m0, n0, ln);
+    // consumed by the next tile's epilogue: the latency hides under its K loop
+    load_row_scales<C>(p, m0 + wm * C::WTM + lrow, rs);
+    // the next tile's first K tile has landed and every wave is done with
+    // the epilogue's LDS
+    dma_wait_barrier<0>();
   }
-
-  // every wave is past its last LDS read of the K loop before LDS is reused
-  __syncthreads();
-  epilogue_lds<C, EPI>(p, acc, m0, n0, wid, wm, wn, lane, reinterpret_cast<unsigned char*>(lds), rs);
 }
-
 
 }  // namespace gemm
 }  // namespace blt

@@ -4,24 +4,41 @@
 namespace blt {
 
 namespace {
-template <int BM, int BN, int BK, int WM, int WN, int S, int OCC, int EPI>
-int run_gemm_dma(const GemmArgs& a, hipStream_t s) {
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int EPI>
+int run_gemm_persistent(const GemmArgs& a, hipStream_t s) {
   const int64_t nb = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm::gemm_bf16_dma_kernel<BM, BN, BK, WM, WN, S, OCC, EPI>),
-                     dim3((unsigned)nb), dim3(64 * WM * WN), 0, s, a);
-  BLT_LAUNCH_CHECK("gemm_bf16_dma_kernel");
+  // one block per CU, a multiple of 8 blocks so each keeps its XCD residue
+  int64_t grid = device_cus();
+  grid = grid >= 8 ? grid & ~7 : grid;
+  if (grid <= 0 || grid > nb) grid = nb;
+  hipLaunchKernelGGL((gemm::gemm_bf16_dma_persistent_kernel<BM, BN, BK, WM, WN, EPI>),
+                     dim3((unsigned)grid), dim3(64 * WM * WN), 0, s, a);
+  BLT_LAUNCH_CHECK("gemm_bf16_dma_persistent_kernel");
   return 0;
 }
 
 // one kernel per epilogue, so each carries only its own registers and code
-template <int BM, int BN, int BK, int WM, int WN, int S, int OCC>
+template <int BM, int BN, int BK, int WM, int WN>
 int run_gemm_dma_epi(const GemmArgs& a, hipStream_t s) {
   switch (a.epi) {
-    case EPI_BF16: return run_gemm_dma<BM, BN, BK, WM, WN, S, OCC, EPI_BF16>(a, s);
-    case EPI_F32: return run_gemm_dma<BM, BN, BK, WM, WN, S, OCC, EPI_F32>(a, s);
-    case EPI_RESID_F32: return run_gemm_dma<BM, BN, BK, WM, WN, S, OCC, EPI_RESID_F32>(a, s);
-    case EPI_QKV_ROPE: return run_gemm_dma<BM, BN, BK, WM, WN, S, OCC, EPI_QKV_ROPE>(a, s);
-    case EPI_SILU_GATE: return run_gemm_dma<BM, BN, BK, WM, WN, S, OCC, EPI_SILU_GATE>(a, s);
+    case EPI_BF16: return run_gemm_persistent<BM, BN, BK, WM, WN, EPI_BF16>(a, s);
+    case EPI_F32: return run_gemm_persistent<BM, BN, BK, WM, WN, EPI_F32>(a, s);
+    case EPI_RESID_F32: return run_gemm_persistent<BM, BN, BK, WM, WN, EPI_RESID_F32>(a, s);
+    case EPI_QKV_ROPE: return run_gemm_persistent<BM, BN, BK, WM, WN, EPI_QKV_ROPE>(a, s);
+    case EPI_SILU_GATE: return run_gemm_persistent<BM, BN, BK, WM, WN, EPI_SILU_GATE>(a, s);
   }
   return fail(-2, "gemm: unknown epilogue");
 }
@@ -54,10 +71,15 @@ int launch_gemm(const GemmArgs& a_in, hipStream_t s) {
   // Wide N (QKV, W1|W3): walk groups of 8 M-tiles so the blocks resident on
   // an XCD share A and Bt tiles in its L2; narrow N (O, W2: 3 tiles): N fastest.
   a.group_m = (a.N + 255) / 256 >= 8 ? 8 : 0;
-  // N % 256 == 0: 256x256 tiles over 8 waves (wave tile 128x64), K tiles of
-  // 64 moved by LDS DMA through 2 stages, LDS-staged epilogue.  Otherwise (the
-  // 260-wide head) 128x128 register-staged tiles over 4 waves.
-  if (a.N % 256 == 0) return run_gemm_dma_epi<256, 256, 64, 2, 4, 2, 2>(a, s);
+  // N % 256 == 0: persistent 256x256 tiles over 8 waves (wave tile 128x64),
+  // K tiles of 64 moved by LDS DMA through 2 stages, LDS-staged epilogue; it
+  // addresses a tile's operand and output rows with 32-bit byte offsets, so
+  // their reach must fit.  Otherwise (the 260-wide head, huge strides)
+  // 128x128 register-staged tiles over 4 waves.
+  const int64_t two31 = int64_t(1) << 31;
+  const bool fits = 256 * (a.lda > a.ldb ? a.lda : a.ldb) * 2 + a.K * 2 < two31 &&
+                    256 * a.ldc * 4 < two31;
+  if (a.N % 256 == 0 && fits) return run_gemm_dma_epi<256, 256, 64, 2, 4>(a, s);
   return run_gemm<128, 128, 32, 2, 2, 2, 3>(a, s);
 }
 
