@@ -597,36 +597,6 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
   }
 }
 
-// Wait until at most N of this wave's vector-memory loads are outstanding and
-// its LDS operations are done, then barrier; the memory clobber keeps the
-// compiler from moving LDS accesses across it.
-template <int N>
-__device__ inline void dma_wait_barrier() {
-  asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-
-// global_load_lds_dwordx4 with a wave-uniform 64-bit base (SGPRs) and a
-// per-lane 32-bit byte offset: lane i's 16 bytes at base + off land at LDS
-// byte lds_addr + 16 * i.  M0 is restored.
-__device__ inline void dma16_so(const void* base_in, unsigned off, unsigned lds_addr) {
-  // the base is wave-uniform by construction; make that explicit so it is
-  // held in SGPRs (readfirstlane returns int: each half goes through
-  // uint32_t so the low word is not sign-extended into the high one)
-  const uint64_t b = (uint64_t)(uintptr_t)base_in;
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
-  const uint64_t base = (uint64_t)lo | ((uint64_t)hi << 32);
-  unsigned saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "global_load_lds_dwordx4 %2, %3\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(lds_addr), "v"(off), "s"(base)
-      : "memory");
-}
-
 // Same tiling and epilogues as gemm_bf16_kernel, but K tiles move global ->
 // LDS by the LDS-DMA path (no VGPR staging, no ds_write) through two LDS
 // stages, and the kernel is persistent: one block per CU walks the tiles

@@ -33,6 +33,7 @@ constexpr int V_LD = 72;    // V row pitch in bf16 (144 B): conflict-free transp
 constexpr int K_TILE = BKV * D;
 constexpr int V_TILE = BKV * V_LD;
 constexpr int STAGE = K_TILE + V_TILE;
+constexpr int NSTAGE = 3;   // LDS stages: one tile consumed, two in flight
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 #define LDS_PTR(p) ((__attribute__((address_space(3))) s16x4_t*)(p))
@@ -47,7 +48,7 @@ template <int NQ>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
   constexpr int QPW = 32 * NQ;
   constexpr int BQ = 4 * QPW;
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[NSTAGE * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int lrow = lane & 31, lhalf = lane >> 5;
@@ -114,48 +115,70 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
       qf[qq][ks] = __builtin_bit_cast(
           bf16x8_t, *reinterpret_cast<const u32x4_t*>(qrow + ks * 16 + lhalf * 8));
   }
-
-  // K/V tile staging: thread -> (key, 16-byte chunk), two chunks each of K and V.
-  // Each thread keeps 32-bit byte offsets of its rows; a tile adds its uniform
-  // row base, so the loads take a scalar base plus a vector offset.  In the
-  // last, partial tile keys past T load key T-1 (masked: a key >= T is never
-  // visible).
-  u32x4_t rk[2], rv[2];
-  uint32_t offk[2], offv[2];
+  // each query's segment start (lower key bound of packed rows)
+  int qseg[NQ];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int id2 = tid + 256 * i, key = id2 >> 3, c = id2 & 7;
-    offk[i] = (uint32_t)(((int64_t)key * p.st_k + c * 8) * 2);
-    offv[i] = (uint32_t)(((int64_t)key * p.st_v + c * 8) * 2);
+  for (int qq = 0; qq < NQ; ++qq) qseg[qq] = p.causal ? seg_at(qw + 32 * qq + lrow) : 0;
+  // Consume the Q and segment loads here, before the K/V DMA is issued: the
+  // compiler counts only its own loads, so a first use inside the tile loop
+  // would wait for every DMA in flight as well.
+#pragma unroll
+  for (int qq = 0; qq < NQ; ++qq) {
+    asm volatile("" ::"v"(qseg[qq]));
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(qf[qq][ks]));
   }
-  auto gload = [&](int t) {
+
+  // K/V tiles move global -> LDS by DMA (global_load_lds_dwordx4: 1 KB per
+  // instruction, lane i's 16 bytes land at slot i) through NSTAGE LDS stages,
+  // two tiles in flight while one is consumed.  A tile is NKOP K ops (8 keys
+  // x 8 chunks each, chunks in the kswz order) and NVOP V ops (64 rows of 9
+  // slots: 8 chunks and a pad slot that fetches chunk 0 again, for the
+  // 144-byte pitch); op o is issued by wave o % 4, so a wave issues ops
+  // q = 0, 1 (K) and 2, 3 (and wave 0 also 4) (V).  Each lane keeps the byte
+  // offset of its piece from the tile's first row; in the last, partial tile
+  // keys past T load key T-1 (masked: a key >= T is never visible).
+  constexpr int NKOP = K_TILE * 2 / 1024, NVOP = V_TILE * 2 / 1024, NOP = NKOP + NVOP;
+  constexpr int QMAX = (NOP + 3) / 4;
+  static_assert(NKOP == 8 && NVOP == 9 && QMAX == 5, "op split assumed below");
+  const int wid_u = __builtin_amdgcn_readfirstlane(wid);
+  const int nops = (NOP - wid_u + 3) / 4;  // 5 for wave 0, 4 for the others
+  const unsigned lds_base = (unsigned)(uintptr_t)lds;
+  uint32_t goff[QMAX];
+  int gkey[QMAX];
+#pragma unroll
+  for (int q = 0; q < QMAX; ++q) {
+    const int o = wid_u + 4 * q;
+    if (q < 2) {
+      const int slot = o * 64 + lane, key = slot >> 3;
+      const int c = (slot & 7) ^ ((key >> 1) & 7);
+      gkey[q] = key;
+      goff[q] = (uint32_t)(((int64_t)key * p.st_k + c * 8) * 2);
+    } else {
+      const int slot = (o - NKOP) * 64 + lane, key = slot / 9, c9 = slot % 9;
+      const int c = c9 < 8 ? c9 : 0;
+      gkey[q] = key < BKV ? key : BKV - 1;
+      goff[q] = (uint32_t)(((int64_t)gkey[q] * p.st_v + c * 8) * 2);
+    }
+  }
+  auto issue = [&](int t, int stage) {
     const int64_t k0 = (int64_t)t * BKV;
     const char* kb0 = reinterpret_cast<const char*>(kbase + k0 * p.st_k);
     const char* vb0 = reinterpret_cast<const char*>(vbase + k0 * p.st_v);
-    if (k0 + BKV <= T) {  // uniform: the whole tile is in range
+    const bool full = k0 + BKV <= T;  // uniform
+    const unsigned sb = lds_base + (unsigned)(stage * STAGE * 2);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        rk[i] = *reinterpret_cast<const u32x4_t*>(kb0 + offk[i]);
-        rv[i] = *reinterpret_cast<const u32x4_t*>(vb0 + offv[i]);
+    for (int q = 0; q < QMAX; ++q) {
+      if (q == QMAX - 1 && nops < QMAX) break;
+      const int o = wid_u + 4 * q;
+      const bool isk = q < 2;
+      uint32_t off = goff[q];
+      if (!full) {
+        const int64_t back = k0 + gkey[q] < T ? 0 : k0 + gkey[q] - (T - 1);  // rows to step back
+        off -= (uint32_t)(back * (isk ? p.st_k : p.st_v) * 2);
       }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int key = (tid + 256 * i) >> 3;
-        const int64_t back = k0 + key < T ? 0 : k0 + key - (T - 1);  // rows to step back
-        rk[i] = *reinterpret_cast<const u32x4_t*>(kb0 + offk[i] - back * p.st_k * 2);
-        rv[i] = *reinterpret_cast<const u32x4_t*>(vb0 + offv[i] - back * p.st_v * 2);
-      }
-    }
-  };
-  auto sstore = [&](int stage) {
-    uint16_t* sk = lds + stage * STAGE;
-    uint16_t* sv = sk + K_TILE;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int id2 = tid + 256 * i, key = id2 >> 3, c = id2 & 7;
-      *reinterpret_cast<u32x4_t*>(sk + kswz(key, c)) = rk[i];
-      *reinterpret_cast<u32x4_t*>(sv + key * V_LD + c * 8) = rv[i];
+      const unsigned la = isk ? sb + (unsigned)(o * 1024) : sb + (unsigned)(K_TILE * 2 + (o - NKOP) * 1024);
+      dma16_so(isk ? kb0 : vb0, off, la);
     }
   };
 
@@ -185,13 +208,18 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
       bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});  // bf16 1.0
   const float sl2 = 0.125f * 1.44269504088896340736f;  // 1/sqrt(64) * log2(e)
 
-  gload(t_begin);
-  sstore(0);
-  __syncthreads();
-
+  issue(t_begin, 0);
+  if (t_begin + 1 <= t_end) issue(t_begin + 1, 1);
+  int stage = 0;  // stage of tile t
   for (int t = t_begin; t <= t_end; ++t) {
-    if (t < t_end) gload(t + 1);
-    const int stage = (t - t_begin) & 1;
+    // tile t has landed (only tile t + 1's ops may still be in flight) and
+    // every wave is past tile t - 1, whose stage now takes tile t + 2
+    if (t + 1 <= t_end) {
+      if (nops == 5) dma_wait_barrier<5>(); else dma_wait_barrier<4>();
+    } else {
+      dma_wait_barrier<0>();
+    }
+    if (t + 2 <= t_end) issue(t + 2, stage == 0 ? NSTAGE - 1 : stage - 1);
     if (wave_active && t >= wt_begin && t <= wt_end) {
       const uint16_t* sk = lds + stage * STAGE;
       const uint16_t* sv = sk + K_TILE;
@@ -241,7 +269,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
         if (mask_lo) {
           int lim_lo = window > 0 ? qi - window : -1;  // key > lim_lo
           if (p.causal) {
-            const int sg = seg_at(qi) - 1;
+            const int sg = qseg[qq] - 1;
             lim_lo = lim_lo > sg ? lim_lo : sg;
           }
           const int lo_rel = lim_lo - kb - 4 * lhalf;
@@ -313,8 +341,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
             lsum[qq] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, pb[qq][sub][u], lsum[qq], 0,
                                                                0, 0);
     }
-    if (t < t_end) sstore((t + 1 - t_begin) & 1);
-    __syncthreads();
+    stage = stage + 1 < NSTAGE ? stage + 1 : 0;
   }
 
   if (!wave_active) return;
@@ -353,6 +380,15 @@ int run_attention(const AttnArgs& a, hipStream_t s) {
 int launch_attention(const AttnArgs& a, hipStream_t s) {
   if (a.B == 0 || a.H == 0 || a.T == 0) return 0;
   if (a.T > 0x3fffffff) return fail(-2, "attention: T too large");
+  // Q/K/V rows move as 16-byte pieces (K/V by LDS DMA)
+  const bool al16 = (uintptr_t)a.q % 16 == 0 && (uintptr_t)a.k % 16 == 0 &&
+                    (uintptr_t)a.v % 16 == 0 && (uintptr_t)a.o % 8 == 0;
+  const bool st8 = a.sb_q % 8 == 0 && a.sh_q % 8 == 0 && a.st_q % 8 == 0 && a.sb_k % 8 == 0 &&
+                   a.sh_k % 8 == 0 && a.st_k % 8 == 0 && a.sb_v % 8 == 0 && a.sh_v % 8 == 0 &&
+                   a.st_v % 8 == 0 && a.sb_o % 4 == 0 && a.sh_o % 4 == 0 && a.st_o % 4 == 0;
+  if (!al16 || !st8)
+    return fail(-2, "attention: q/k/v need 16-byte aligned rows (pointers 16-byte aligned, "
+                    "strides multiples of 8 elements)");
   // K/V rows of a tile are addressed by 32-bit byte offsets from the tile base
   const int64_t st = a.st_k > a.st_v ? a.st_k : a.st_v;
   if ((st * (BKV - 1) + D) * 2 >= ((int64_t)1 << 32))
