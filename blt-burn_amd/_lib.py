@@ -66,6 +66,9 @@ EXPORTS = {
     "blt_gemm_bf16": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp]),
     "blt_gemm_bf16_epilogue": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                        c_i32, c_i32, c_i32, c_i64, c_vp, c_vp]),
+    "blt_probe_mfma_flops": (c_i64, [c_i32, c_i32]),
+    "blt_probe_mfma_bf16": (c_i32, [c_i32, c_i32, c_vp, c_vp]),
+    "blt_probe_copy": (c_i32, [c_vp, c_vp, c_i64, c_vp]),
 }
 
 

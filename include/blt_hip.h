@@ -376,6 +376,18 @@ int blt_gemm_bf16_epilogue(const uint16_t* A, const uint16_t* Bt, void* C, int64
                            int32_t n_valid, int32_t rope_cols, int64_t seq_len,
                            const float* rope_cs, blt_stream_t stream);
 
+/* Measurement helpers (no counterpart in the reference; bench.py reads the
+ * rates this GPU sustains beside the published peaks) --------------------- */
+
+/* FLOPs of one blt_probe_mfma_bf16 launch (-1 on bad arguments). */
+int64_t blt_probe_mfma_flops(int32_t blocks, int32_t iters);
+/* `blocks` blocks of 4 wave64s, each wave running iters x 4 independent
+ * v_mfma_f32_32x32x16_bf16; sink (>= blocks * 256 floats) is never written in
+ * practice. */
+int blt_probe_mfma_bf16(int32_t blocks, int32_t iters, float* sink, blt_stream_t stream);
+/* dst = src, `bytes` (a multiple of 16) with 16-byte loads and stores. */
+int blt_probe_copy(const void* src, void* dst, int64_t bytes, blt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

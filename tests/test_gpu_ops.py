@@ -292,3 +292,19 @@ def test_gemm_f32_epilogue_partial_columns(M, N):
     _gemm_epi(a, bt, c, _lib.EPI_F32, n_valid=N)
     ref = a.float() @ bt.float().t()
     assert (c - ref).abs().max().item() <= 2e-3 * ref.abs().max().item()
+
+
+# ---------------------------------------------------------------- measurement probes
+def test_probe_copy_and_mfma():
+    L = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    x = torch.randn(1 << 20, device=DEV)
+    y = torch.empty_like(x)
+    _lib.check(L.blt_probe_copy(x.data_ptr(), y.data_ptr(), x.numel() * 4, stream), "probe_copy")
+    sink = torch.zeros(8 * 256, device=DEV)
+    _lib.check(L.blt_probe_mfma_bf16(8, 16, sink.data_ptr(), stream), "probe_mfma")
+    torch.cuda.synchronize()
+    assert torch.equal(x, y)
+    assert sink.abs().sum().item() == 0.0  # the sink is never written
+    assert L.blt_probe_mfma_flops(8, 16) == 8 * 4 * 16 * 4 * 32 * 32 * 16 * 2
+    assert L.blt_probe_copy(x.data_ptr(), y.data_ptr(), 10, stream) != 0  # not a multiple of 16
