@@ -58,7 +58,7 @@ def _dispatch_stages(names, layers):
             out.append("attention")
         elif "rmsnorm" in n:
             out.append("rmsnorm")
-        elif "entropy_kernel" in n:
+        elif "entropy_" in n and "_kernel" in n:
             out.append("entropy")
         elif "patch_boundary_kernel" in n:
             out.append("patch_boundaries")
@@ -415,7 +415,7 @@ def bench_config1(args):
         "data": "synthetic: logits ~ N(0, 2.0), seed %d" % synth.config_seed(1),
         "config": {"workload": "config1: fused_entropy + patch boundaries (global 1.33, "
                                "monotonic 0.2)", "batch": B, "seq_len": T, "vocab": V},
-        "roofline": _with_achievable({"bound": "hbm", "kernel": "entropy_kernel",
+        "roofline": _with_achievable({"bound": "hbm", "kernel": "entropy_tail_kernel",
                                       "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                                       "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                                       "traffic": None, "launch_ms": round(ms_ent, 4),

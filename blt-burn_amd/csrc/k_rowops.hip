@@ -102,6 +102,54 @@ __global__ __launch_bounds__(256) void entropy_kernel(const T* __restrict__ logi
   if (lane == 0) out[row] = -h;
 }
 
+// Rows of n = 256 NF + 64 (VT - 1) + r elements (n % 4 == 0, NF <= 4, VT <= 4):
+// NF full chunks of 256 (16-byte loads, 4 per lane) and a tail of VT
+// elements per lane (e = 256 NF + 64 q + lane), so no lane computes an
+// exponential for a chunk that is mostly padding.  One exponential per
+// element: with d = x - max, p = exp(d), s = sum p, lse = log s,
+//   H = -sum (p / s)(d - lse) = lse - (sum p d) / s,
+// the same quantity as -sum exp(lsm) lsm (padding: p = 0, d clamped finite).
+template <typename T, int NF, int VT>
+__global__ __launch_bounds__(256) void entropy_tail_kernel(const T* __restrict__ logits,
+                                                           float* __restrict__ out,
+                                                           int64_t rows, int n) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* x = logits + row * n;
+  float v[NF > 0 ? NF : 1][4], t[VT > 0 ? VT : 1];
+#pragma unroll
+  for (int c = 0; c < NF; ++c) ld4(x, c * 256 + lane * 4, v[c]);
+#pragma unroll
+  for (int q = 0; q < VT; ++q) {
+    const int e = NF * 256 + q * 64 + lane;
+    t[q] = e < n ? ld1(x, e) : -INFINITY;
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < NF; ++c)
+    m = fmaxf(m, fmaxf(fmaxf(v[c][0], v[c][1]), fmaxf(v[c][2], v[c][3])));
+#pragma unroll
+  for (int q = 0; q < VT; ++q) m = fmaxf(m, t[q]);
+  m = wave_max(m);
+  float sp = 0.f, sd = 0.f;
+  auto acc = [&](float xv) {
+    const float d = fmaxf(xv - m, -1e30f);  // padding (-inf) contributes 0
+    const float pe = __expf(d);
+    sp += pe;
+    sd = fmaf(pe, d, sd);
+  };
+#pragma unroll
+  for (int c = 0; c < NF; ++c)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc(v[c][k]);
+#pragma unroll
+  for (int q = 0; q < VT; ++q) acc(t[q]);
+  sp = wave_sum(sp);
+  sd = wave_sum(sd);
+  if (lane == 0) out[row] = __logf(sp) - sd / sp;
+}
+
 // Any width: three streaming passes over the row.
 template <typename T>
 __global__ __launch_bounds__(256) void entropy_stream_kernel(const T* __restrict__ logits,
@@ -416,7 +464,7 @@ __global__ __launch_bounds__(256) void rope64_kernel(const uint16_t* __restrict_
 // starts into lengths (patch_lengths_from_start_indices, patcher.rs:144-164).
 // ---------------------------------------------------------------------------
 #define PB_THREADS 1024
-#define PB_ITEMS 8
+#define PB_ITEMS 8  // the vector path below loads and stores them as two 16-byte pieces
 
 // Row b covers H[off_b, off_b + T_b): off_b = b * T and T_b = T for a dense
 // [B, T] input, or row_off[b] / row_len[b] for variable-length rows (the
@@ -428,33 +476,66 @@ __global__ __launch_bounds__(PB_THREADS) void patch_boundary_kernel(
     int32_t* __restrict__ count, const int64_t* __restrict__ row_off,
     const int32_t* __restrict__ row_len) {
   __shared__ int wave_tot[PB_THREADS / BLT_WAVE];
-  __shared__ int carry_s;
+  // this chunk's starts (chunk-local order), so lengths need no global
+  // write-then-read round trip; the last start of a chunk waits for the
+  // first start of a later chunk (or the row end)
+  __shared__ int32_t chunk_starts[PB_THREADS * PB_ITEMS];
+  __shared__ int carry_s, chunk_tot_s, pend_idx_s, pend_start_s;
   const int64_t b = blockIdx.x;
   const int64_t roff = row_off ? row_off[b] : b * T_dense;
   const int64_t T = row_len ? (int64_t)row_len[b] : T_dense;
   const float* h = H + roff;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  if (tid == 0) carry_s = 0;
+  const bool want_len = lengths && starts;
+  if (tid == 0) {
+    carry_s = 0;
+    pend_idx_s = -1;
+    pend_start_s = 0;
+  }
   __syncthreads();
   for (int64_t t0 = 0; t0 < T; t0 += (int64_t)PB_THREADS * PB_ITEMS) {
     const int64_t p0 = t0 + (int64_t)tid * PB_ITEMS;
     int flags[PB_ITEMS];
     int local = 0;
     float prev = (p0 >= 1 && p0 - 1 < T) ? h[p0 - 1] : 0.f;
+    // whole 16-byte pieces when the row is aligned and this thread's items
+    // all exist (PB_ITEMS == 8: two float4 loads, two int4 mask stores)
+    const bool full = p0 + PB_ITEMS <= T;
+    const bool vec = full && ((uintptr_t)h & 15) == 0;
+    const bool vec_st = full && ((uintptr_t)(mask + roff) & 15) == 0;
+    float cur[PB_ITEMS];
+    if (vec) {
+      const float4 a = *reinterpret_cast<const float4*>(h + p0);
+      const float4 c = *reinterpret_cast<const float4*>(h + p0 + 4);
+      cur[0] = a.x; cur[1] = a.y; cur[2] = a.z; cur[3] = a.w;
+      cur[4] = c.x; cur[5] = c.y; cur[6] = c.z; cur[7] = c.w;
+    } else {
+#pragma unroll
+      for (int k = 0; k < PB_ITEMS; ++k) cur[k] = p0 + k < T ? h[p0 + k] : 0.f;
+    }
 #pragma unroll
     for (int k = 0; k < PB_ITEMS; ++k) {
       const int64_t t = p0 + k;
       int f = 0;
       if (t < T) {
-        const float cur = h[t];
         if (t < 2) f = 1;
-        else if (mode == 0) f = (cur - prev) > thr;
-        else f = cur > thr;
-        prev = cur;
-        if (mask) mask[roff + t] = f;
+        else if (mode == 0) f = (cur[k] - prev) > thr;
+        else f = cur[k] > thr;
+        prev = cur[k];
       }
       flags[k] = f;
       local += f;
+    }
+    if (mask) {
+      if (vec_st) {
+        *reinterpret_cast<int4*>(mask + roff + p0) = int4{flags[0], flags[1], flags[2], flags[3]};
+        *reinterpret_cast<int4*>(mask + roff + p0 + 4) =
+            int4{flags[4], flags[5], flags[6], flags[7]};
+      } else {
+#pragma unroll
+        for (int k = 0; k < PB_ITEMS; ++k)
+          if (p0 + k < T) mask[roff + p0 + k] = flags[k];
+      }
     }
     // inclusive wave scan of per-thread counts
     int incl = local;
@@ -474,29 +555,37 @@ __global__ __launch_bounds__(PB_THREADS) void patch_boundary_kernel(
         if (lane >= off) wincl += v;
       }
       if (lane < PB_THREADS / BLT_WAVE) wave_tot[lane] = wincl - wt;  // exclusive
+      if (lane == PB_THREADS / BLT_WAVE - 1) chunk_tot_s = wincl;
     }
     __syncthreads();
-    const int carry = carry_s;
-    int pos = carry + wave_tot[wid] + (incl - local);
+    const int carry = carry_s, n_chunk = chunk_tot_s;
+    int loc = wave_tot[wid] + (incl - local);  // chunk-local index of this thread's first start
     if (starts) {
 #pragma unroll
       for (int k = 0; k < PB_ITEMS; ++k)
-        if (flags[k]) starts[roff + pos++] = (int32_t)(p0 + k);
+        if (flags[k]) {
+          starts[roff + carry + loc] = (int32_t)(p0 + k);
+          chunk_starts[loc] = (int32_t)(p0 + k);
+          ++loc;
+        }
     }
-    __syncthreads();
-    if (tid == PB_THREADS - 1) carry_s = carry + wave_tot[wid] + incl;
-    __syncthreads();
+    __syncthreads();  // chunk_starts complete; every thread has read carry_s
+    if (want_len && n_chunk > 0) {
+      for (int i = tid; i + 1 < n_chunk; i += PB_THREADS)
+        lengths[roff + carry + i] = chunk_starts[i + 1] - chunk_starts[i];
+      if (tid == 0) {
+        if (pend_idx_s >= 0) lengths[roff + pend_idx_s] = chunk_starts[0] - pend_start_s;
+        pend_idx_s = carry + n_chunk - 1;
+        pend_start_s = chunk_starts[n_chunk - 1];
+      }
+    }
+    if (tid == 0) carry_s = carry + n_chunk;
+    __syncthreads();  // chunk_starts, carry_s and the pending start are reused next chunk
   }
   const int n = carry_s;
-  if (tid == 0 && count) count[b] = n;
-  if (lengths && starts) {
-    __threadfence_block();
-    __syncthreads();
-    for (int i = tid; i < n; i += PB_THREADS) {
-      const int32_t s = starts[roff + i];
-      const int32_t e = (i + 1 < n) ? starts[roff + i + 1] : (int32_t)T;
-      lengths[roff + i] = e - s;
-    }
+  if (tid == 0) {
+    if (count) count[b] = n;
+    if (want_len && pend_idx_s >= 0) lengths[roff + pend_idx_s] = (int32_t)T - pend_start_s;
   }
 }
 
@@ -588,6 +677,36 @@ struct EntropyL {
     BLT_LAUNCH_CHECK("entropy_stream_kernel");
     return 0;
   }
+  template <int NF, int VT>
+  static int tail(const Args& a) {
+    hipLaunchKernelGGL((entropy_tail_kernel<T, NF, VT>), dim3(ceil_div(a.rows, 4)), dim3(256), 0,
+                       a.s, a.x, a.out, a.rows, a.n);
+    BLT_LAUNCH_CHECK("entropy_tail_kernel");
+    return 0;
+  }
+  template <int NF>
+  static int tail_vt(const Args& a, int vt) {
+    switch (vt) {
+      case 0: return NF > 0 ? tail<NF, 0>(a) : -1;
+      case 1: return tail<NF, 1>(a);
+      case 2: return tail<NF, 2>(a);
+      case 3: return tail<NF, 3>(a);
+      case 4: return tail<NF, 4>(a);
+    }
+    return -1;
+  }
+  // n % 4 == 0 with 16-byte (f32) / 8-byte (bf16) aligned rows, n < 1280
+  static int fast(const Args& a) {
+    const int nf = a.n / 256, vt = (a.n % 256 + 63) / 64;
+    switch (nf) {
+      case 0: return tail_vt<0>(a, vt);
+      case 1: return tail_vt<1>(a, vt);
+      case 2: return tail_vt<2>(a, vt);
+      case 3: return tail_vt<3>(a, vt);
+      case 4: return tail_vt<4>(a, vt);
+    }
+    return -1;
+  }
 };
 
 template <typename TX, typename TW, typename TY>
@@ -642,10 +761,14 @@ unsigned elementwise_grid(int64_t work) {
 
 int launch_entropy_f32(const float* x, float* out, int64_t rows, int n, hipStream_t s) {
   if (rows == 0) return 0;
+  if (n > 0 && n % 4 == 0 && n < 1280 && aligned(x, 16))
+    return EntropyL<float>::fast({x, out, rows, n, s});
   return dispatch_row<EntropyL<float>>(n, aligned(x, 16), {x, out, rows, n, s});
 }
 int launch_entropy_bf16(const uint16_t* x, float* out, int64_t rows, int n, hipStream_t s) {
   if (rows == 0) return 0;
+  if (n > 0 && n % 4 == 0 && n < 1280 && aligned(x, 8))
+    return EntropyL<uint16_t>::fast({x, out, rows, n, s});
   return dispatch_row<EntropyL<uint16_t>>(n, aligned(x, 8), {x, out, rows, n, s});
 }
 

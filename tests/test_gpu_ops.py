@@ -53,6 +53,18 @@ def test_entropy_vs_oracle(shape, std, mean):
     np.testing.assert_allclose(H, ref, atol=1e-4)  # reference tests: 1e-4 / 1e-3
 
 
+@pytest.mark.parametrize("n", [4, 64, 68, 128, 256, 260, 320, 512, 516, 1024, 1280])
+@pytest.mark.parametrize("std", [0.5, 8.0])
+def test_entropy_widths_vs_oracle(n, std):
+    # every (full chunks, tail) split of the one-exponential kernel; std 8 gives
+    # near one-hot rows, where H = lse - sum(p d) / s must not cancel badly
+    x = synth.normal_f32(31 + n, (3, 17, n), 1.0, std)
+    H = F.fused_entropy(cuda(x), n).cpu().numpy()
+    np.testing.assert_allclose(H, oracle.entropy(x), atol=1e-4)
+    xb, xf = bf16(x)
+    np.testing.assert_allclose(F.fused_entropy(xb, n).cpu().numpy(), oracle.entropy(xf), atol=1e-4)
+
+
 def test_entropy_config1_full_size():
     # logits f32 [4, 8192, 260] ~ N(0, 2)
     x = synth.normal_f32(synth.config_seed(1), (4, 8192, 260), 0.0, 2.0)
