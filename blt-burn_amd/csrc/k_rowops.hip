@@ -202,7 +202,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const TX* __restrict__ x,
 #pragma unroll
     for (int q = 0; q < VEC; ++q) ss += r.v[c][q] * r.v[c][q];
   ss = wave_sum(ss);
-  const float den = rms_denominator(ss, n, eps, mode);
+  // x / den as x * (1 / den): one correctly rounded reciprocal per row
+  // instead of an IEEE division per element (within 1.5 ulp of the quotient)
+  const float inv = 1.f / rms_denominator(ss, n, eps, mode);
   if (l2 != nullptr && lane == 0) l2[row] = sqrtf(ss);
   if (y == nullptr) return;
   TY* yr = y + row * n;
@@ -214,7 +216,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const TX* __restrict__ x,
       if constexpr (VEC == 4) ld4(w, e, wv);
       else wv[0] = ld1(w, e);
 #pragma unroll
-      for (int q = 0; q < VEC; ++q) o[q] = (r.v[c][q] / den) * wv[q];
+      for (int q = 0; q < VEC; ++q) o[q] = (r.v[c][q] * inv) * wv[q];
       if constexpr (VEC == 4) st4(yr, e, o);
       else st1(yr, e, o[0]);
     }
@@ -238,10 +240,10 @@ __global__ __launch_bounds__(256) void rmsnorm_stream_kernel(const TX* __restric
     ss += v * v;
   }
   ss = wave_sum(ss);
-  const float den = rms_denominator(ss, n, eps, mode);
+  const float inv = 1.f / rms_denominator(ss, n, eps, mode);
   if (l2 != nullptr && lane == 0) l2[row] = sqrtf(ss);
   if (y == nullptr) return;
-  for (int e = lane; e < n; e += BLT_WAVE) st1(y + row * n, e, (ld1(xr, e) / den) * ld1(w, e));
+  for (int e = lane; e < n; e += BLT_WAVE) st1(y + row * n, e, (ld1(xr, e) * inv) * ld1(w, e));
 }
 
 // ---------------------------------------------------------------------------
