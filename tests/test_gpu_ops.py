@@ -320,3 +320,35 @@ def test_probe_copy_and_mfma():
     assert sink.abs().sum().item() == 0.0  # the sink is never written
     assert L.blt_probe_mfma_flops(8, 16) == 8 * 4 * 16 * 4 * 32 * 32 * 16 * 2
     assert L.blt_probe_copy(x.data_ptr(), y.data_ptr(), 10, stream) != 0  # not a multiple of 16
+
+
+# ---------------------------------------------------------------- persistent GEMM tile walks
+@pytest.mark.parametrize("K", [64, 192, 320, 768])
+def test_gemm_persistent_many_tiles_odd_k_tiles(K):
+    # More tiles than CUs (each block walks several tiles) with odd and even
+    # numbers of 64-deep K tiles, so the LDS stage holding a tile's last K
+    # tile alternates between tiles; a ragged last row tile.  Every epilogue
+    # kind on the same operands.
+    M, N = 256 * 133 + 17, 512
+    torch.manual_seed(K)
+    a = torch.randn(M, K, device=DEV).to(torch.bfloat16)
+    bt = (0.1 * torch.randn(N, K, device=DEV)).to(torch.bfloat16)
+    y = a.float() @ bt.float().t()
+    tol = lambda ref: 2 ** -7 * ref.abs().max().item() + 1e-3
+
+    c = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+    _gemm_epi(a, bt, c, _lib.EPI_BF16)
+    assert (c.float() - y).abs().max().item() <= tol(y)
+
+    r0 = torch.randn(M, N, device=DEV)
+    r = r0.clone()
+    _gemm_epi(a, bt, r, _lib.EPI_RESID_F32)
+    ref = r0 + y
+    assert (r - ref).abs().max().item() <= 2e-3 * ref.abs().max().item()
+
+    h = torch.empty(M, N // 2, device=DEV, dtype=torch.bfloat16)
+    _gemm_epi(a, bt, h, _lib.EPI_SILU_GATE)
+    g = y.view(M, N // 64, 2, 32)[:, :, 0, :].reshape(M, N // 2)
+    u = y.view(M, N // 64, 2, 32)[:, :, 1, :].reshape(M, N // 2)
+    ref = torch.nn.functional.silu(g) * u
+    assert (h.float() - ref).abs().max().item() <= tol(ref)
