@@ -396,10 +396,25 @@ void gemm_bf16_kernel(GemmArgs p) {
 // waits for the wave's outstanding LDS operations.
 __device__ inline void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// RoPE (cos, sin) pairs of this lane's 16 frequencies (8 g + 4 (lane / 32) + e)
+// for output row `row` of the QKV projection.
+__device__ inline void load_rope_cs(const GemmArgs& p, int64_t row, int lane, f32x4_t (&cs)[8]) {
+  const int64_t pos = rope_pos(p, row);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float* t = p.rope_cs + (pos * 32 + 8 * g + 4 * (lane >> 5)) * 2;
+    cs[2 * g] = *reinterpret_cast<const f32x4_t*>(t);
+    cs[2 * g + 1] = *reinterpret_cast<const f32x4_t*>(t + 4);
+  }
+}
+
+// cs0: the table pairs of the lane's first row block, loaded by the caller
+// ahead of time (QKV only).
 template <class C, int EPI>
 __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C::TN], int64_t m0,
                                     int64_t n0, int wid, int wm, int wn, int lane,
-                                    unsigned char* smem, const float (&rs)[C::TM]) {
+                                    unsigned char* smem, const float (&rs)[C::TM],
+                                    const f32x4_t (&cs0)[8]) {
   const int lrow = lane & 31, lhalf = lane >> 5;
   const int64_t row0 = m0 + wm * C::WTM;  // first row of this wave's tile
   const int64_t col0 = n0 + wn * C::WTN;  // first column (pre-epilogue index)
@@ -499,16 +514,11 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
   // RoPE (cos, sin) pairs of this lane's 16 frequencies (8 g + 4 lhalf + e)
   // for its row of tile row i, loaded one row ahead
   f32x4_t cscur[8], csnext[8];
-  auto load_cs = [&](int i) {
-    const int64_t pos = rope_pos(p, row0 + i * 32 + lrow);
+  auto load_cs = [&](int i) { load_rope_cs(p, row0 + i * 32 + lrow, lane, csnext); };
+  if (rope) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const float* cs = p.rope_cs + (pos * 32 + 8 * g + 4 * lhalf) * 2;
-      csnext[2 * g] = *reinterpret_cast<const f32x4_t*>(cs);
-      csnext[2 * g + 1] = *reinterpret_cast<const f32x4_t*>(cs + 4);
-    }
-  };
-  if (rope) load_cs(0);
+    for (int t = 0; t < 8; ++t) csnext[t] = cs0[t];
+  }
 #pragma unroll
   for (int i0 = 0; i0 < C::TM; i0 += 2) {
 #pragma unroll
@@ -682,6 +692,7 @@ void gemm_bf16_dma_persistent_kernel(GemmArgs p) {
       bfr[j] = *reinterpret_cast<const bf16x8_t*>(sb + swz<BK>(wn * C::WTN + j * 32 + lrow, chunk));
   };
   f32x16_t acc[C::TM][C::TN];
+  f32x4_t cs0[8];  // QKV: the RoPE pairs of the epilogue's first row block
   // Fragments are double-buffered: the LDS reads of K step ks + 1 are issued
   // before the MFMAs of step ks, and scheduling barriers keep the compiler
   // from sinking them back next to their uses, so each wave has LDS reads in
@@ -733,6 +744,8 @@ void gemm_bf16_dma_persistent_kernel(GemmArgs p) {
         set_tile(m0n, n0n, ln);
         dma_tile(0, st ^ 1);
       }
+      if (EPI == EPI_QKV_ROPE && kt + 1 == KT && n0 + wn * C::WTN < p.rope_cols)
+        load_rope_cs(p, m0 + wm * C::WTM + lrow, lane, cs0);
       compute(st);
       if (kt + 1 < KT) dma_wait_barrier<0>();
       st ^= 1;
@@ -744,7 +757,7 @@ void gemm_bf16_dma_persistent_kernel(GemmArgs p) {
     // the loop (hoisted out, it would occupy registers through the K loop)
     int le = lane;
     asm volatile("" : "+v"(le));
-    epilogue_lds<C, EPI>(p, acc, m0, n0, wid, wm, wn, le, lds + (st == 0 ? SB : 0), rs);
+    epilogue_lds<C, EPI>(p, acc, m0, n0, wid, wm, wn, le, lds + (st == 0 ? SB : 0), rs, cs0);
     if (!more) break;
     v = vn;
     m0 = m0n;
