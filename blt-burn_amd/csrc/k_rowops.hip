@@ -7,6 +7,8 @@
 // exactly once and all reductions are wave shuffles.  Rows wider than the
 // register budget fall back to a streaming variant that re-reads the row.
 #include "../../include/blt_hip.h"
+#include <type_traits>
+
 #include "rowops.hpp"
 
 #include <math.h>
@@ -219,6 +221,75 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const TX* __restrict__ x,
       for (int q = 0; q < VEC; ++q) o[q] = (r.v[c][q] * inv) * wv[q];
       if constexpr (VEC == 4) st4(yr, e, o);
       else st1(yr, e, o[0]);
+    }
+  }
+}
+
+// bf16 rows of n <= 1024 (n % 8 == 0), two rows per wave in 16-byte pieces:
+// piece p = lane + 64 k covers row p / (n / 8), elements 8 (p % (n / 8)) ..
+// + 8, so the wave's loads and stores are whole 16-byte pieces (the generic
+// kernel moves 8 bytes per lane for bf16) and both rows' reads are in flight
+// together.
+template <int NP>
+__global__ __launch_bounds__(256) void rmsnorm_bf16_pair_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
+    float* __restrict__ l2, int64_t rows, int n, float eps, int mode) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 2;
+  if (row0 >= rows) return;
+  const int pr = n / 8;                       // pieces per row
+  const int np = row0 + 1 < rows ? 2 * pr : pr;  // pieces of this wave's rows
+  u32x4_t xv[NP];
+  float ss0 = 0.f, ss1 = 0.f;
+#pragma unroll
+  for (int k = 0; k < NP; ++k) {
+    const int p = lane + 64 * k;
+    if (p < np) {
+      const int r = p >= pr, c = (p - r * pr) * 8;
+      xv[k] = *reinterpret_cast<const u32x4_t*>(x + (row0 + r) * n + c);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NP; ++k) {
+    const int p = lane + 64 * k;
+    if (p < np) {
+      float q = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = bf16_to_f32((uint16_t)(xv[k][e] & 0xffff));
+        const float hi = bf16_to_f32((uint16_t)(xv[k][e] >> 16));
+        q += lo * lo + hi * hi;
+      }
+      if (p >= pr) ss1 += q; else ss0 += q;
+    }
+  }
+  ss0 = wave_sum(ss0);
+  ss1 = wave_sum(ss1);
+  // x / den as x * (1 / den), as the generic kernel
+  const float inv0 = 1.f / rms_denominator(ss0, n, eps, mode);
+  const float inv1 = 1.f / rms_denominator(ss1, n, eps, mode);
+  if (l2 != nullptr && lane == 0) {
+    l2[row0] = sqrtf(ss0);
+    if (row0 + 1 < rows) l2[row0 + 1] = sqrtf(ss1);
+  }
+  if (y == nullptr) return;
+#pragma unroll
+  for (int k = 0; k < NP; ++k) {
+    const int p = lane + 64 * k;
+    if (p < np) {
+      const int r = p >= pr, c = (p - r * pr) * 8;
+      const float inv = r ? inv1 : inv0;
+      const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(w + c);
+      u32x4_t o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x0 = bf16_to_f32((uint16_t)(xv[k][e] & 0xffff));
+        const float x1 = bf16_to_f32((uint16_t)(xv[k][e] >> 16));
+        const float w0 = bf16_to_f32((uint16_t)(wv[e] & 0xffff));
+        const float w1 = bf16_to_f32((uint16_t)(wv[e] >> 16));
+        o[e] = pack_bf16x2((x0 * inv) * w0, (x1 * inv) * w1);
+      }
+      *reinterpret_cast<u32x4_t*>(y + (row0 + r) * n + c) = o;
     }
   }
 }
@@ -778,6 +849,26 @@ template <typename TX, typename TW, typename TY>
 int launch_rmsnorm(const TX* x, const TW* w, TY* y, float* l2, int64_t rows, int n, float eps,
                    int mode, hipStream_t s) {
   if (rows == 0) return 0;
+  if constexpr (std::is_same<TX, uint16_t>::value && std::is_same<TW, uint16_t>::value &&
+                std::is_same<TY, uint16_t>::value) {
+    if (n % 8 == 0 && n > 0 && n <= 1024 && aligned(x, 16) && aligned(w, 16) &&
+        (y == nullptr || aligned(y, 16))) {
+      const unsigned grid = ceil_div(rows, 8);
+      const int np = (2 * (n / 8) + 63) / 64;
+#define BLT_RMS_PAIR(NP)                                                                 \
+  hipLaunchKernelGGL(rmsnorm_bf16_pair_kernel<NP>, dim3(grid), dim3(256), 0, s, x, w, y, l2, \
+                     rows, n, eps, mode);                                                \
+  BLT_LAUNCH_CHECK("rmsnorm_bf16_pair_kernel");                                          \
+  return 0;
+      switch (np) {
+        case 1: BLT_RMS_PAIR(1)
+        case 2: BLT_RMS_PAIR(2)
+        case 3: BLT_RMS_PAIR(3)
+        default: BLT_RMS_PAIR(4)
+      }
+#undef BLT_RMS_PAIR
+    }
+  }
   const bool vec = aligned(x, 4 * sizeof(TX)) && aligned(w, 4 * sizeof(TW)) &&
                    aligned(y, 4 * sizeof(TY));
   return dispatch_row<RmsL<TX, TW, TY>>(n, vec, {x, w, y, l2, rows, n, eps, mode, s});

@@ -102,6 +102,19 @@ def test_rms_norm_bf16_config2():
     np.testing.assert_allclose(l2.cpu().numpy(), oracle.l2_norm(xf), rtol=1e-5)
 
 
+@pytest.mark.parametrize("dim", [8, 64, 760, 768, 1024, 1032])
+@pytest.mark.parametrize("rows", [1, 7, 130])
+def test_rms_norm_bf16_widths(dim, rows):
+    # the two-rows-per-wave bf16 kernel (n % 8 == 0, n <= 1024; odd row counts
+    # leave a wave with one row) and the generic kernel beyond it
+    xb, xf = bf16(synth.normal_f32(40 + dim, (1, rows, dim)))
+    wb, wf = bf16(synth.normal_f32(41 + dim, dim, 1.0, 0.02))
+    l2 = torch.empty((1, rows), dtype=torch.float32, device=DEV)
+    y = F.fused_rms_norm(xb, wb, 1e-5, F.EPS_AFTER_SQRT, l2_out=l2).float().cpu().numpy()
+    np.testing.assert_allclose(y, oracle.rms_norm(xf, wf, 1e-5, 0), rtol=2 ** -8, atol=1e-6)
+    np.testing.assert_allclose(l2.cpu().numpy(), oracle.l2_norm(xf), rtol=1e-5)
+
+
 def test_l2_norm():
     x = synth.normal_f32(15, (2, 16, 128))  # test_fused_ops.rs:63-94
     np.testing.assert_allclose(F.fused_l2_norm(cuda(x)).cpu().numpy(), oracle.l2_norm(x),
