@@ -147,6 +147,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--ingest-mib", type=float, default=24.0,
                     help="config 5: MiB of the seeded 1 GiB document stream to ingest per pass")
+    ap.add_argument("--ingest-segment-mib", type=float, default=64.0,
+                    help="config 5: documents go to the ingest driver in document-aligned "
+                         "segments of about this many MiB (bounds host memory for the "
+                         "outputs; one progress line per segment on stderr)")
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--seq", type=int, default=8192)
     ap.add_argument("--window", type=int, default=512)
@@ -627,6 +631,15 @@ def bench_ingest(args):
     nbytes = int(args.ingest_mib * 2 ** 20)
     data, off = synth.documents(seed, nbytes)
     wdata, woff = synth.documents(seed + 1, 2 ** 20)
+    # document-aligned segments of about --ingest-segment-mib each
+    seg = max(1, int(args.ingest_segment_mib * 2 ** 20))
+    cuts = np.searchsorted(off, np.arange(seg, int(off[-1]), seg), side="left")
+    cuts = np.unique(np.concatenate([[0], cuts[(cuts > 0) & (cuts < off.size - 1)],
+                                     [off.size - 1]]))
+    segments = list(zip(cuts[:-1].tolist(), cuts[1:].tolist()))
+    if len(segments) > 1:
+        print("config 5: %d documents, %.1f MiB in %d segments" % (
+            off.size - 1, off[-1] / 2 ** 20, len(segments)), file=sys.stderr, flush=True)
 
     def one_pass(d, o):
         toks, toff = tk.tokenize_documents(d, o, conf.add_bos, conf.add_eos)
@@ -636,13 +649,23 @@ def bench_ingest(args):
         one_pass(wdata, woff)
     model.read_profile()
     model.set_profiling(True)
+    st = {}
     t0 = time.perf_counter()
     for _ in range(steps):
-        res = one_pass(data, off)
+        st = {}
+        for k, (d0, d1) in enumerate(segments):
+            r = one_pass(data[off[d0]:off[d1]], off[d0:d1 + 1] - off[d0])
+            if k == 0:
+                res = r  # the parity sample below reads the first documents
+            for name, v in ing.last_stats().items():
+                st[name] = st.get(name, 0) + v
+            if len(segments) > 1:
+                print("config 5: segment %d/%d done, %.1f s" % (
+                    k + 1, len(segments), time.perf_counter() - t0), file=sys.stderr, flush=True)
+            del r
     t1 = time.perf_counter()
     prof = model.read_profile()
     model.set_profiling(False)
-    st = ing.last_stats()
     sec = (t1 - t0) / steps
     gpu_ms = sum(ms for ms, n in prof.values()) / steps
     dom = "w13_gemm_silu"
@@ -657,7 +680,8 @@ def bench_ingest(args):
         "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: %.1f MiB prefix of the seeded config-5 document stream "
-                "(%d documents), random-init bf16 weights" % (nbytes / 2 ** 20, off.size - 1),
+                "(%d documents, %d segment(s)), random-init bf16 weights" % (
+                    nbytes / 2 ** 20, off.size - 1, len(segments)),
         "config": {"workload": "config5: tokenize + chunk/overlap + packed forward + stitch + "
                                "per-document monotonic boundaries, host in / host out",
                    "rows": B, "row_len": T, "chunk_len": T, "overlap": 512, "window": W,
