@@ -286,7 +286,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
         for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
           for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[qq][sub][r]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * sl2;
+        {
+          // the partner lane (lane ^ 32) holds the other 32 keys of this
+          // query: one VALU lane swap instead of an LDS permute round trip
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt),
+                                                           __float_as_uint(mt), false, false);
+          mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * sl2;
+        }
         if (__any(mt > m[qq] + 8.f)) {
           const float m_new = fmaxf(m[qq], mt);
           const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[qq] - m_new);
