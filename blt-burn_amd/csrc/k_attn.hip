@@ -57,13 +57,14 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
   // keep them on one XCD (dispatch places block i on XCD i % 8).
   const int T = (int)p.T;
   const int nqb = (T + BQ - 1) / BQ;
-  const int64_t nb = (int64_t)nqb * p.H * p.B;
-  const int64_t bid = blockIdx.x;
-  const int64_t nb8 = nb & ~(int64_t)7;
-  const int64_t id = bid < nb8 ? (bid & 7) * (nb8 >> 3) + (bid >> 3) : bid;
-  const int qb = nqb - 1 - (int)(id % nqb);  // longest causal rows first
-  const int64_t bh = id / nqb;
-  const int64_t h = bh % p.H, b = bh / p.H;
+  // 32-bit block decode: the launcher keeps the grid below 2^31 blocks
+  const uint32_t nb = (uint32_t)nqb * (uint32_t)p.H * (uint32_t)p.B;
+  const uint32_t bid = blockIdx.x;
+  const uint32_t nb8 = nb & ~7u;
+  const uint32_t id = bid < nb8 ? (bid & 7) * (nb8 >> 3) + (bid >> 3) : bid;
+  const int qb = nqb - 1 - (int)(id % (uint32_t)nqb);  // longest causal rows first
+  const uint32_t bh = id / (uint32_t)nqb;
+  const int64_t h = bh % (uint32_t)p.H, b = bh / (uint32_t)p.H;
 
   const int q0 = qb * BQ;
   const int qw = q0 + wid * QPW;  // this wave's first query
@@ -153,12 +154,12 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
       const int slot = o * 64 + lane, key = slot >> 3;
       const int c = (slot & 7) ^ ((key >> 1) & 7);
       gkey[q] = key;
-      goff[q] = (uint32_t)(((int64_t)key * p.st_k + c * 8) * 2);
+      goff[q] = ((uint32_t)key * (uint32_t)p.st_k + c * 8) * 2;  // < 2^32 (launcher)
     } else {
       const int slot = (o - NKOP) * 64 + lane, key = slot / 9, c9 = slot % 9;
       const int c = c9 < 8 ? c9 : 0;
       gkey[q] = key < BKV ? key : BKV - 1;
-      goff[q] = (uint32_t)(((int64_t)gkey[q] * p.st_v + c * 8) * 2);
+      goff[q] = ((uint32_t)gkey[q] * (uint32_t)p.st_v + c * 8) * 2;
     }
   }
   auto issue = [&](int t, int stage) {
@@ -356,7 +357,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
     const int qi = qw + 32 * qq + lrow;
     if (qi >= T) continue;
     const float lt = lsum[qq][0];
-    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    // hardware reciprocal (1 ulp): the output is rounded to bf16
+    const float inv = lt > 0.f ? __builtin_amdgcn_rcpf(lt) : 0.f;
     uint16_t* orow = p.o + b * p.sb_o + h * p.sh_o + (int64_t)qi * p.st_o;
 #pragma unroll
     for (int dsub = 0; dsub < 2; ++dsub)
