@@ -65,15 +65,58 @@ __device__ inline uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 // ---- wave64 reductions -----------------------------------------------------
-__device__ inline float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, BLT_WAVE));
+// All on the VALU (no LDS permutes): DPP quad permutes pair lanes xor 1 and
+// xor 2, the row half-mirror pairs the two quads of each 8 lanes and the row
+// mirror the two halves of each 16 lanes; v_permlane16_swap / v_permlane32_swap
+// then hand each lane its partner in the neighbouring 16- and 32-lane group.
+// Each step combines a lane's value with exactly one partner and both
+// partners compute the same (commutative) result, so every lane of the group
+// ends with the identical value.
+template <int CTRL>
+__device__ inline float dpp_f32(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+// {own, partner} of lane ^ 16 (X = 16) or lane ^ 32 (X = 32), in some order
+template <int X>
+__device__ inline void swap_pair(float v, float& a, float& b) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  if constexpr (X == 16) {
+    const auto s = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    a = __builtin_bit_cast(float, (unsigned)s[0]);
+    b = __builtin_bit_cast(float, (unsigned)s[1]);
+  } else {
+    const auto s = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    a = __builtin_bit_cast(float, (unsigned)s[0]);
+    b = __builtin_bit_cast(float, (unsigned)s[1]);
+  }
+}
+// sum over each aligned group of 16 lanes, in every lane of the group
+__device__ inline float sum16(float v) {
+  v += dpp_f32<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_f32<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_f32<0x141>(v);  // row_half_mirror
+  v += dpp_f32<0x140>(v);  // row_mirror
   return v;
 }
 __device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, BLT_WAVE);
-  return v;
+  v = sum16(v);
+  float a, b;
+  swap_pair<16>(v, a, b);
+  v = a + b;
+  swap_pair<32>(v, a, b);
+  return a + b;
+}
+__device__ inline float wave_max(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  float a, b;
+  swap_pair<16>(v, a, b);
+  v = fmaxf(a, b);
+  swap_pair<32>(v, a, b);
+  return fmaxf(a, b);
 }
 
 inline unsigned ceil_div(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }

@@ -100,21 +100,6 @@ __device__ inline void scale_rows(f32x16_t (&acc)[C::TM][C::TN], const float (&r
       for (int e = 0; e < 16; ++e) acc[i][j][e] *= rs[i];
 }
 
-// Sum over each aligned group of 16 lanes, result in every lane of the group:
-// DPP quad permutes (xor 1, xor 2), then mirrors within 8 and within 16 lanes.
-template <int CTRL>
-__device__ inline float dpp_f32(float x) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
-}
-__device__ inline float sum16(float v) {
-  v += dpp_f32<0xB1>(v);   // quad_perm [1, 0, 3, 2]
-  v += dpp_f32<0x4E>(v);   // quad_perm [2, 3, 0, 1]
-  v += dpp_f32<0x141>(v);  // row_half_mirror
-  v += dpp_f32<0x140>(v);  // row_mirror
-  return v;
-}
-
 template <class C>
 __device__ inline void epilogue(const GemmArgs& p, f32x16_t (&acc)[C::TM][C::TN], int64_t m0,
                                 int64_t n0, int wm, int wn, int lrow, int lhalf,

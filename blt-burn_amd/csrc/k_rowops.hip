@@ -149,7 +149,8 @@ __global__ __launch_bounds__(256) void entropy_tail_kernel(const T* __restrict__
   for (int q = 0; q < VT; ++q) acc(t[q]);
   sp = wave_sum(sp);
   sd = wave_sum(sd);
-  if (lane == 0) out[row] = __logf(sp) - sd / sp;
+  // hardware reciprocal (1 ulp) for the one quotient per row
+  if (lane == 0) out[row] = __logf(sp) - sd * __builtin_amdgcn_rcpf(sp);
 }
 
 // Any width: three streaming passes over the row.
@@ -459,8 +460,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ 
       *reinterpret_cast<u32x2_t*>(xb + row * dim + e) =
           *reinterpret_cast<const u32x2_t*>(src + e);
       float q = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
-#pragma unroll
-      for (int m = 8; m >= 1; m >>= 1) q += __shfl_xor(q, m, BLT_WAVE);
+      q = sum16(q);
       if ((lane & 15) == 0) ss[row * (dim / 64) + e / 64] = q;
     }
   }
