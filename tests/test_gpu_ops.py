@@ -245,6 +245,46 @@ def test_attention_vs_oracle(B, H, T, causal, window, theta):
     np.testing.assert_allclose(o, ref, atol=2e-2, rtol=0)
 
 
+def test_entropy_boundaries_graph_replay():
+    # fused_entropy + both boundary passes captured as one HIP graph; every
+    # replay (with eager work and syncs between them) matches the eager step
+    B, T, V = 2, 3000, 260
+    logits = cuda(synth.normal_f32(71, (B, T, V), 0.0, 2.0))
+    outs = [tuple(torch.empty(s, dtype=torch.int32, device=DEV)
+                  for s in ((B, T), (B, T), (B, T), (B,))) for _ in range(2)]
+    held = {}
+
+    def step():
+        H = F.fused_entropy(logits, V)
+        held["H"] = H
+        patcher.patch_boundaries(H, 1.33, patcher.PATCH_GLOBAL, out=outs[0])
+        patcher.patch_boundaries(H, 0.2, patcher.PATCH_MONOTONIC, out=outs[1])
+
+    step()
+    torch.cuda.synchronize()
+    eager = [t.clone() for t in (held["H"],) + outs[0] + outs[1]]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for k in range(3):
+        for t in outs[0] + outs[1]:
+            t.fill_(-7)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (held["H"],) + outs[0] + outs[1]
+        for i, (a, b) in enumerate(zip(eager, got)):
+            if i in (2, 3, 6, 7):  # starts / lengths: only the first counts[b] entries are defined
+                cnt = eager[4 if i < 4 else 8].cpu().numpy()
+                for r in range(B):
+                    np.testing.assert_array_equal(a[r, :cnt[r]].cpu().numpy(),
+                                                  b[r, :cnt[r]].cpu().numpy())
+            else:
+                assert torch.equal(a, b), (k, i)
+        # eager work between replays
+        F.fused_entropy(cuda(synth.normal_f32(72 + k, (1, 64, V))), V)
+        torch.cuda.synchronize()
+
+
 def test_attention_config3_b1():
     # config 3 shape at B=1 (the CPU comparison size): T=4096, 12 heads, window 512, RoPE
     o, ref = _attn_case(1, 12, 4096, True, 512, 10000.0, seed=synth.config_seed(3))
