@@ -240,14 +240,17 @@ __global__ __launch_bounds__(256) void rmsnorm_bf16_pair_kernel(
   if (row0 >= rows) return;
   const int pr = n / 8;                       // pieces per row
   const int np = row0 + 1 < rows ? 2 * pr : pr;  // pieces of this wave's rows
-  u32x4_t xv[NP];
+  u32x4_t xv[NP], wv[NP];
   float ss0 = 0.f, ss1 = 0.f;
+  // the weight pieces are loaded with the row pieces, so the stores after the
+  // reductions wait on nothing further
 #pragma unroll
   for (int k = 0; k < NP; ++k) {
     const int p = lane + 64 * k;
     if (p < np) {
       const int r = p >= pr, c = (p - r * pr) * 8;
       xv[k] = *reinterpret_cast<const u32x4_t*>(x + (row0 + r) * n + c);
+      if (y != nullptr) wv[k] = *reinterpret_cast<const u32x4_t*>(w + c);
     }
   }
 #pragma unroll
@@ -280,14 +283,13 @@ __global__ __launch_bounds__(256) void rmsnorm_bf16_pair_kernel(
     if (p < np) {
       const int r = p >= pr, c = (p - r * pr) * 8;
       const float inv = r ? inv1 : inv0;
-      const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(w + c);
       u32x4_t o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float x0 = bf16_to_f32((uint16_t)(xv[k][e] & 0xffff));
         const float x1 = bf16_to_f32((uint16_t)(xv[k][e] >> 16));
-        const float w0 = bf16_to_f32((uint16_t)(wv[e] & 0xffff));
-        const float w1 = bf16_to_f32((uint16_t)(wv[e] >> 16));
+        const float w0 = bf16_to_f32((uint16_t)(wv[k][e] & 0xffff));
+        const float w1 = bf16_to_f32((uint16_t)(wv[k][e] >> 16));
         o[e] = pack_bf16x2((x0 * inv) * w0, (x1 * inv) * w1);
       }
       *reinterpret_cast<u32x4_t*>(y + (row0 + r) * n + c) = o;
