@@ -107,6 +107,26 @@ __device__ inline float wave_sum(float v) {
   swap_pair<32>(v, a, b);
   return a + b;
 }
+// Inclusive prefix sums on the VALU (GFX9 DPP; lanes with no source add 0):
+// row_shr 1, 2, 4, 8 within each 16-lane row, then row_bcast:15 (last lane of
+// rows 0 / 2 into rows 1 / 3) and row_bcast:31 (lane 31 into rows 2 and 3).
+template <int CTRL, int ROWS>
+__device__ inline int dpp_i32(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, ROWS, 0xF, false);
+}
+__device__ inline int row16_incl_scan(int v) {
+  v += dpp_i32<0x111, 0xF>(v);
+  v += dpp_i32<0x112, 0xF>(v);
+  v += dpp_i32<0x114, 0xF>(v);
+  v += dpp_i32<0x118, 0xF>(v);
+  return v;
+}
+__device__ inline int wave_incl_scan(int v) {
+  v = row16_incl_scan(v);
+  v += dpp_i32<0x142, 0xA>(v);
+  v += dpp_i32<0x143, 0xC>(v);
+  return v;
+}
 __device__ inline float wave_max(float v) {
   v = fmaxf(v, dpp_f32<0xB1>(v));
   v = fmaxf(v, dpp_f32<0x4E>(v));

@@ -613,22 +613,13 @@ __global__ __launch_bounds__(PB_THREADS) void patch_boundary_kernel(
       }
     }
     // inclusive wave scan of per-thread counts
-    int incl = local;
-#pragma unroll
-    for (int off = 1; off < BLT_WAVE; off <<= 1) {
-      const int v = __shfl_up(incl, off, BLT_WAVE);
-      if (lane >= off) incl += v;
-    }
+    const int incl = wave_incl_scan(local);
     if (lane == BLT_WAVE - 1) wave_tot[wid] = incl;
     __syncthreads();
     if (wid == 0) {
-      int wt = lane < PB_THREADS / BLT_WAVE ? wave_tot[lane] : 0;
-      int wincl = wt;
-#pragma unroll
-      for (int off = 1; off < PB_THREADS / BLT_WAVE; off <<= 1) {
-        const int v = __shfl_up(wincl, off, BLT_WAVE);
-        if (lane >= off) wincl += v;
-      }
+      static_assert(PB_THREADS / BLT_WAVE == 16, "wave totals scanned within one 16-lane row");
+      const int wt = lane < PB_THREADS / BLT_WAVE ? wave_tot[lane] : 0;
+      const int wincl = row16_incl_scan(wt);
       if (lane < PB_THREADS / BLT_WAVE) wave_tot[lane] = wincl - wt;  // exclusive
       if (lane == PB_THREADS / BLT_WAVE - 1) chunk_tot_s = wincl;
     }
