@@ -537,14 +537,19 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
             x2[e] = acc[i][j + 1][4 * g + e] * rs[i];
           }
           if (silu) {
-            // silu(g) * u = g / (1 + e^-g) * u, with the hardware exp2 and
+            // silu(g) * u with g = rs a1, u = rs a2 (rs > 0, the row factor):
+            //   g / (1 + e^-g) * u = (a1 a2) / ((1 + e^-g) / rs^2),
+            // four VALU ops per output beside the hardware exp2 and
             // reciprocal (about 1 ulp each)
+            const float k1 = rs[i] * -1.44269504f;
+            const float irs2 = __builtin_amdgcn_rcpf(rs[i] * rs[i]);
             float o[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              o[e] = x1[e] *
-                     __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x1[e] * 1.44269504f)) *
-                     x2[e];
+            for (int e = 0; e < 4; ++e) {
+              const float a1 = acc[i][j][4 * g + e], a2 = acc[i][j + 1][4 * g + e];
+              const float ex = __builtin_amdgcn_exp2f(a1 * k1);
+              o[e] = (a1 * a2) * __builtin_amdgcn_rcpf(fmaf(ex, irs2, irs2));
+            }
             *reinterpret_cast<u32x2_t*>(buf + rl * LD + (j / 2) * 32 + 8 * g + 4 * lhalf) =
                 u32x2_t{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
           } else {
