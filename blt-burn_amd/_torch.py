@@ -5,7 +5,17 @@ import torch
 from ._lib import BltError
 
 
+# the raw current-stream handle without building a torch.cuda.Stream object
+# (one per call otherwise: about 1.5 us of host time on every launch)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device=None):
+    if _raw_stream is not None:
+        if isinstance(device, torch.device) and device.index is not None:
+            return _raw_stream(device.index)
+        if device is None or isinstance(device, int):
+            return _raw_stream(torch.cuda.current_device() if device is None else device)
     return torch.cuda.current_stream(device).cuda_stream
 
 

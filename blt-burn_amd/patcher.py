@@ -31,13 +31,13 @@ def patch_boundaries(entropies, threshold, mode=PATCH_MONOTONIC, out=None):
     require_cuda(entropies)
     if entropies.dim() != 2:
         raise BltError("patch_boundaries expects [batch, seq]")
-    H = contiguous(entropies.to(torch.float32))
+    H = contiguous(entropies if entropies.dtype == torch.float32 else entropies.to(torch.float32))
     B, T = H.shape
     if out is not None:
         mask, starts, lengths, counts = out
         for t, shp in ((mask, (B, T)), (starts, (B, T)), (lengths, (B, T)), (counts, (B,))):
             require_cuda(t)
-            if tuple(t.shape) != shp or t.dtype != torch.int32 or not t.is_contiguous():
+            if t.shape != shp or t.dtype != torch.int32 or not t.is_contiguous():
                 raise BltError("patch_boundaries: out tensors must be contiguous int32")
     else:
         mask = torch.empty((B, T), dtype=torch.int32, device=H.device)
