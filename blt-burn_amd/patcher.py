@@ -35,9 +35,11 @@ def patch_boundaries(entropies, threshold, mode=PATCH_MONOTONIC, out=None):
     B, T = H.shape
     if out is not None:
         mask, starts, lengths, counts = out
+        i32 = torch.int32
         for t, shp in ((mask, (B, T)), (starts, (B, T)), (lengths, (B, T)), (counts, (B,))):
-            require_cuda(t)
-            if t.shape != shp or t.dtype != torch.int32 or not t.is_contiguous():
+            if not (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == i32 and
+                    t.shape == shp and t.is_contiguous()):
+                require_cuda(t)
                 raise BltError("patch_boundaries: out tensors must be contiguous int32")
     else:
         mask = torch.empty((B, T), dtype=torch.int32, device=H.device)
