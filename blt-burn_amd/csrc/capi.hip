@@ -264,18 +264,18 @@ int blt_fused_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_
   a.sb_o = sb_o; a.sh_o = sh_o; a.st_o = st_o;
   a.causal = causal ? 1 : 0; a.window = window;
   if (rope_theta > 0.f) {
-    // rotate q and k into dense head-major copies in the workspace
+    // k is rotated into a dense head-major copy in the workspace (each K row
+    // is read by many query blocks); q is rotated inside the attention kernel
+    // as it is loaded (once per query)
     if (workspace == nullptr)
       return fail(BLT_ERR_INVALID, "fused_attention: rope needs a workspace");
-    uint16_t* qr = reinterpret_cast<uint16_t*>(workspace);
-    uint16_t* kr = qr + B * H * T * d;
+    uint16_t* kr = reinterpret_cast<uint16_t*>(workspace) + B * H * T * d;
     const float* cs = nullptr;
     int rc;
     if ((rc = rope_table_device(d, T, rope_theta, &cs))) return rc;
-    if ((rc = launch_rope(q, qr, cs, B, H, T, d, sb_q, sh_q, st_q, s))) return rc;
     if ((rc = launch_rope(k, kr, cs, B, H, T, d, sb_kv, sh_kv, st_kv, s))) return rc;
-    a.q = qr; a.sb_q = H * T * d; a.sh_q = T * d; a.st_q = d;
     a.k = kr; a.sb_k = H * T * d; a.sh_k = T * d; a.st_k = d;
+    a.q_rope_cs = cs;
   }
   return launch_attention(a, s);
 }

@@ -115,6 +115,30 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
     for (int ks = 0; ks < 4; ++ks)
       qf[qq][ks] = __builtin_bit_cast(
           bf16x8_t, *reinterpret_cast<const u32x4_t*>(qrow + ks * 16 + lhalf * 8));
+    if (p.q_rope_cs) {
+      // fragments ks and ks + 2 hold the pair halves m and m + 32 of the same
+      // 8 frequencies m = 16 ks + 8 lhalf + e: rotate them in registers
+      const float* cs = p.q_rope_cs + (int64_t)qc * 64;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const f32x4_t* t = reinterpret_cast<const f32x4_t*>(cs + (16 * ks + 8 * lhalf) * 2);
+        const u32x4_t lo = __builtin_bit_cast(u32x4_t, qf[qq][ks]);
+        const u32x4_t hi = __builtin_bit_cast(u32x4_t, qf[qq][ks + 2]);
+        u32x4_t o1, o2;
+#pragma unroll
+        for (int q2 = 0; q2 < 4; ++q2) {  // pairs 2 q2, 2 q2 + 1
+          const f32x4_t c = t[q2];        // (cos, sin) of pair 2 q2, then of pair 2 q2 + 1
+          const float a0 = bf16_to_f32((uint16_t)(lo[q2] & 0xffff));
+          const float a1 = bf16_to_f32((uint16_t)(lo[q2] >> 16));
+          const float b0 = bf16_to_f32((uint16_t)(hi[q2] & 0xffff));
+          const float b1 = bf16_to_f32((uint16_t)(hi[q2] >> 16));
+          o1[q2] = pack_bf16x2(a0 * c.x - b0 * c.y, a1 * c.z - b1 * c.w);
+          o2[q2] = pack_bf16x2(a0 * c.y + b0 * c.x, a1 * c.w + b1 * c.z);
+        }
+        qf[qq][ks] = __builtin_bit_cast(bf16x8_t, o1);
+        qf[qq][ks + 2] = __builtin_bit_cast(bf16x8_t, o2);
+      }
+    }
   }
   // each query's segment start (lower key bound of packed rows)
   int qseg[NQ];

@@ -94,6 +94,9 @@ struct AttnArgs {
   // the first token of t's segment, non-decreasing along a row.  Key j is
   // visible to query i only if j >= seg_start[i].  NULL = one segment per row.
   const int32_t* seg_start;
+  // Optional: q is rotated (half-split RoPE pairs (m, m + 32)) as it is loaded,
+  // with the (cos, sin) table [T, 32, 2] f32 at the query's row index.
+  const float* q_rope_cs;
 };
 int launch_attention(const AttnArgs& a, hipStream_t s);
 
