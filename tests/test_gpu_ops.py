@@ -245,6 +245,29 @@ def test_attention_vs_oracle(B, H, T, causal, window, theta):
     np.testing.assert_allclose(o, ref, atol=2e-2, rtol=0)
 
 
+def test_attention_rope_64_query_waves():
+    # long full-causal rows take the 64-queries-per-wave kernel; with RoPE its q
+    # is rotated in registers as it is loaded.  Same result as handing it q and
+    # k rotated beforehand (half-split pairs, the oracle's f32 table).
+    B, H, T = 4, 16, 4096
+    qb, _ = bf16(synth.normal_f32(81, (B, H, T, 64)))
+    kb, _ = bf16(synth.normal_f32(82, (B, H, T, 64)))
+    vb, _ = bf16(synth.normal_f32(83, (B, H, T, 64)))
+    cs = torch.from_numpy(np.ascontiguousarray(oracle.rope_table(64, T, 10000.0))).to(DEV)
+    cs = cs.reshape(T, 32, 2)
+    c, s_ = cs[..., 0], cs[..., 1]
+
+    def rot(x):
+        x = x.float()
+        x1, x2 = x[..., :32], x[..., 32:]
+        return torch.cat([x1 * c - x2 * s_, x1 * s_ + x2 * c], dim=-1).to(torch.bfloat16)
+
+    o = F.fused_attention(qb, kb, vb, True, rope_theta=10000.0).float()
+    ref = F.fused_attention(rot(qb), rot(kb), vb, True).float()
+    # the two paths differ only in where each rotated value was rounded to bf16
+    assert float((o - ref).abs().max()) < 2e-2
+
+
 def test_entropy_boundaries_graph_replay():
     # fused_entropy + both boundary passes captured as one HIP graph; every
     # replay (with eager work and syncs between them) matches the eager step
