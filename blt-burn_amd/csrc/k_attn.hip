@@ -2,7 +2,8 @@
 // operands on MFMA, f32 online softmax.
 //
 // One block = 4 wave64s = 128 or 256 queries of one (batch, head); K/V
-// advance in 64-key tiles through two LDS stages shared by the four waves.
+// advance in 64-key tiles through three LDS stages shared by the four waves
+// (moved by LDS DMA, two tiles in flight while one is consumed).
 //
 // Each wave computes S^T = K . Q^T (v_mfma_f32_32x32x16_bf16, keys as rows,
 // its 32 queries as columns), so a lane owns one query column and 32 of the
