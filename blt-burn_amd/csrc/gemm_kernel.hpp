@@ -72,7 +72,9 @@ struct GemmCfg {
 // RoPE position of output row `row` (a token of a [B, seq_len] batch): its
 // index in the row, minus its segment's start when rows are packed.
 __device__ inline int64_t rope_pos(const GemmArgs& p, int64_t row) {
-  const int64_t t = row % p.seq_len;
+  // 32-bit: the launcher keeps rows (incl. a last tile's overhang) and
+  // seq_len below 2^31
+  const int64_t t = (int64_t)((uint32_t)row % (uint32_t)p.seq_len);
   if (!p.seg_start) return t;
   int64_t s = p.seg_start[row < p.M ? row : p.M - 1];
   s = s < 0 ? 0 : (s > t ? t : s);

@@ -62,6 +62,10 @@ int launch_gemm(const GemmArgs& a_in, hipStream_t s) {
        a.epi == EPI_SILU_GATE) && (a.N % 64 != 0 || a.ldc % 4 != 0 || (uintptr_t)a.C % 16 != 0))
     return fail(-2, "gemm: vector epilogues need N % 64 == 0, ldc % 4 == 0, 16-byte aligned C");
   if (a.K % 64 != 0) return fail(-2, "gemm: K must be a multiple of 64");
+  if (a.M >= (int64_t(1) << 31) - 256) return fail(-2, "gemm: M must be below 2^31 - 256");
+  if (a.epi == EPI_QKV_ROPE && a.rope_cols > 0 &&
+      (a.seq_len <= 0 || a.seq_len >= (int64_t(1) << 31)))
+    return fail(-2, "gemm: the RoPE epilogue needs 0 < seq_len < 2^31");
   if ((a.xb_out != nullptr) != (a.ss_out != nullptr) ||
       (a.xb_out && (a.epi != EPI_RESID_F32 || a.ss_np * 64 != a.N || (uintptr_t)a.xb_out % 8)))
     return fail(-2, "gemm: norm partials need EPI_RESID_F32, xb_out and ss_out, ss_np = N / 64");
