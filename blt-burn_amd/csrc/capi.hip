@@ -198,7 +198,7 @@ int blt_fused_coherence_f32(const float* norms, const float* entropies, float* o
 // ---- attention ---------------------------------------------------------------
 int64_t blt_attention_workspace_bytes(int64_t B, int64_t H, int64_t T, int32_t d) {
   if (B < 0 || H < 0 || T < 0 || d <= 0) return 0;
-  return 2 * B * H * T * d * 2 + T * d * 4 + 256;
+  return B * H * T * d * 2 + T * d * 4 + 256;  // the rotated k copy (q is rotated in the kernel)
 }
 
 // RoPE tables of the fused attention entry, one per (device, head_dim, theta):
@@ -269,7 +269,7 @@ int blt_fused_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_
     // as it is loaded (once per query)
     if (workspace == nullptr)
       return fail(BLT_ERR_INVALID, "fused_attention: rope needs a workspace");
-    uint16_t* kr = reinterpret_cast<uint16_t*>(workspace) + B * H * T * d;
+    uint16_t* kr = reinterpret_cast<uint16_t*>(workspace);
     const float* cs = nullptr;
     int rc;
     if ((rc = rope_table_device(d, T, rope_theta, &cs))) return rc;
