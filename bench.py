@@ -631,37 +631,32 @@ def bench_ingest(args):
     nbytes = int(args.ingest_mib * 2 ** 20)
     data, off = synth.documents(seed, nbytes)
     wdata, woff = synth.documents(seed + 1, 2 ** 20)
-    # document-aligned segments of about --ingest-segment-mib each
+    # documents go to the ingest driver in segments of about
+    # --ingest-segment-mib; a background thread reads and tokenizes segment
+    # i + 1 while segment i runs on the GPU (ingest.StreamingIngest.stream)
     seg = max(1, int(args.ingest_segment_mib * 2 ** 20))
-    cuts = np.searchsorted(off, np.arange(seg, int(off[-1]), seg), side="left")
-    cuts = np.unique(np.concatenate([[0], cuts[(cuts > 0) & (cuts < off.size - 1)],
-                                     [off.size - 1]]))
-    segments = list(zip(cuts[:-1].tolist(), cuts[1:].tolist()))
-    if len(segments) > 1:
-        print("config 5: %d documents, %.1f MiB in %d segments" % (
-            off.size - 1, off[-1] / 2 ** 20, len(segments)), file=sys.stderr, flush=True)
+    n_seg = max(1, -(-int(off[-1]) // seg))
 
-    def one_pass(d, o):
-        toks, toff = tk.tokenize_documents(d, o, conf.add_bos, conf.add_eos)
-        return ing.run(toks, toff)
+    def docs(d, o):
+        return ((str(i), d[o[i]:o[i + 1]].tobytes()) for i in range(o.size - 1))
 
     for _ in range(args.warmup):
-        one_pass(wdata, woff)
+        for _seg in ing.stream(docs(wdata, woff), seg):
+            pass
     model.read_profile()
     model.set_profiling(True)
     st = {}
     t0 = time.perf_counter()
     for _ in range(steps):
         st = {}
-        for k, (d0, d1) in enumerate(segments):
-            r = one_pass(data[off[d0]:off[d1]], off[d0:d1 + 1] - off[d0])
+        for k, (_ids, _toks, r) in enumerate(ing.stream(docs(data, off), seg)):
             if k == 0:
                 res = r  # the parity sample below reads the first documents
             for name, v in ing.last_stats().items():
                 st[name] = st.get(name, 0) + v
-            if len(segments) > 1:
-                print("config 5: segment %d/%d done, %.1f s" % (
-                    k + 1, len(segments), time.perf_counter() - t0), file=sys.stderr, flush=True)
+            if n_seg > 1:
+                print("config 5: segment %d/~%d done, %.1f s" % (
+                    k + 1, n_seg, time.perf_counter() - t0), file=sys.stderr, flush=True)
             del r
     t1 = time.perf_counter()
     prof = model.read_profile()
@@ -681,9 +676,10 @@ def bench_ingest(args):
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: %.1f MiB prefix of the seeded config-5 document stream "
                 "(%d documents, %d segment(s)), random-init bf16 weights" % (
-                    nbytes / 2 ** 20, off.size - 1, len(segments)),
-        "config": {"workload": "config5: tokenize + chunk/overlap + packed forward + stitch + "
-                               "per-document monotonic boundaries, host in / host out",
+                    nbytes / 2 ** 20, off.size - 1, n_seg),
+        "config": {"workload": "config5: tokenize (background thread) + chunk/overlap + packed "
+                               "forward + stitch + per-document monotonic boundaries, host in / "
+                               "host out",
                    "rows": B, "row_len": T, "chunk_len": T, "overlap": 512, "window": W,
                    "threshold": args.threshold},
         "ingest": {"batches": st["batches"], "documents": st["documents"],

@@ -134,8 +134,10 @@ __device__ inline void epilogue(const GemmArgs& p, f32x16_t (&acc)[C::TM][C::TN]
           x.w += acc[i][j][4 * g + 3];
           *o = x;
           if (p.xb_out) {
+            f32x4_t y = x;
+            if (p.col_scale) y *= *reinterpret_cast<const f32x4_t*>(p.col_scale + col);
             *reinterpret_cast<u32x2_t*>(p.xb_out + row * p.ldc + col) =
-                u32x2_t{pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w)};
+                u32x2_t{pack_bf16x2(y.x, y.y), pack_bf16x2(y.z, y.w)};
             ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
           }
         }
@@ -159,6 +161,9 @@ __device__ inline void epilogue(const GemmArgs& p, f32x16_t (&acc)[C::TM][C::TN]
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int64_t col = col_base + j * 32 + 8 * g;  // first of 4 columns, first half
+          // N % 64 == 0: a 64-column pair group lies wholly inside or wholly
+          // past N (the last N tile of a 128-wide block can overhang by 64)
+          if (col >= p.N) continue;
           float x1[4], x2[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -438,6 +443,13 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
       }
     };
     if (resid) load_resid(0);
+    // the consumer's norm weight for this lane's 4 columns (the same columns
+    // in every slab: 64 | 64 * t), applied to the bf16 copy only
+    f32x4_t csc = f32x4_t{1.f, 1.f, 1.f, 1.f};
+    if (resid && p.col_scale) {
+      const int c = (lane % CPR) * 4;
+      csc = *reinterpret_cast<const f32x4_t*>(p.col_scale + col0 + (c < nrem ? c : nrem - 4));
+    }
 #pragma unroll
     for (int i = 0; i < C::TM; ++i) {
 #pragma unroll
@@ -469,8 +481,9 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
           if (resid) {
             *reinterpret_cast<f32x4_t*>(o) = v[t];
             if (xbb) {
+              const f32x4_t y = v[t] * csc;
               *reinterpret_cast<u32x2_t*>(xbb + off * 2u) =
-                  u32x2_t{pack_bf16x2(v[t].x, v[t].y), pack_bf16x2(v[t].z, v[t].w)};
+                  u32x2_t{pack_bf16x2(y.x, y.y), pack_bf16x2(y.z, y.w)};
               ss = v[t].x * v[t].x + v[t].y * v[t].y + v[t].z * v[t].z + v[t].w * v[t].w;
             }
           } else if (col0 + c + 3 < p.n_valid && p.vec_ok) {

@@ -14,14 +14,19 @@
 //
 // Here the chunks of many documents are packed into [rows, row_len] batches
 // (per-segment attention and RoPE positions keep every chunk independent, as
-// the reference's one-chunk-per-forward loop does), and a whole document
-// always lands in one batch so its boundary pass runs on the device right
-// after the forward.  Host packing of batch i+1 overlaps the GPU work of
-// batch i: two slots of pinned host + device buffers, uploads on one stream,
-// the model on a compute stream, downloads on a third, events between them.
+// the reference's one-chunk-per-forward loop does).  A document whose chunks
+// fit one batch lands in one batch, so its boundary pass runs on the device
+// right after the forward.  A longer one is cut into groups of consecutive
+// chunks that each fit a batch; the groups run in any batches, their stitched
+// outputs are gathered on the host, and the document's boundary pass runs on
+// the device once its last group has landed.  Host packing of batch i+1
+// overlaps the GPU work of batch i: two slots of pinned host + device
+// buffers, uploads on one stream, the model on a compute stream, downloads on
+// a third, events between them.
 #include <string.h>
 
 #include <algorithm>
+#include <map>
 #include <vector>
 
 #include "model.hpp"
@@ -78,6 +83,24 @@ static bool pack_chunks(const std::vector<ChunkPlan>& c, std::vector<int64_t>& f
 // offsets, so the order of batches does not matter).
 static constexpr size_t kLookahead = 1024;
 
+// A packing unit: chunks [c0, c1) of document `doc`'s plan, whose kept outputs
+// are the document positions [out_lo, out_lo + out_len).  `whole` units hold
+// every chunk of their document.
+struct Unit {
+  int64_t doc;
+  int32_t c0, c1;
+  int64_t out_lo, out_len;
+  int64_t computed;  // tokens run through the model
+  bool whole;
+};
+
+// Host gather of a document that spans batches: stitched entropies / norms /
+// coherence until its last unit lands.
+struct LongDoc {
+  int64_t remaining = 0;  // units not yet finished
+  std::vector<float> H, N, C;
+};
+
 struct Ingest {
   Model* m = nullptr;
   blt_ingest_config cfg{};
@@ -124,12 +147,31 @@ struct Ingest {
     float* d_pC = nullptr;
     hipEvent_t uploaded = nullptr, computed = nullptr, done = nullptr;
     bool busy = false;
-    std::vector<int64_t> docs;  // caller's document ids in this batch
-    int64_t out_tokens = 0;     // tokens of those documents
+    std::vector<int64_t> units;  // ids of the units in this batch
+    int64_t out_tokens = 0;      // outputs of those units
   } slot[2];
+
+  // this run's packing units and the documents that span batches
+  std::vector<Unit> units;
+  std::map<int64_t, LongDoc> longs;
+  // device buffers of the boundary pass of a document that spans batches
+  // (grown to the longest such document)
+  int64_t long_cap = 0;
+  float* l_H = nullptr;
+  float* l_N = nullptr;
+  float* l_C = nullptr;
+  int32_t* l_starts = nullptr;
+  int32_t* l_lens = nullptr;
+  float* l_pH = nullptr;
+  float* l_pN = nullptr;
+  float* l_pC = nullptr;
+  int64_t* l_off = nullptr;  // [1] = 0
+  int32_t* l_len = nullptr;  // [1]
+  int32_t* l_count = nullptr;
 
   ~Ingest();
   int init(Model* model, const blt_ingest_config& c);
+  void drain();  // waits for both slots and drops what they hold
   // per-patch outputs of a run (document d's patches at doc_off[d] .. + counts[d])
   struct PatchOut {
     float* ent = nullptr;
@@ -142,6 +184,10 @@ struct Ingest {
           const PatchOut& pm);
   int finish(Slot& s, const int64_t* doc_off, float* ent, float* nrm, float* coh, float* emb,
              int32_t* starts, int32_t* lens, int32_t* counts, const PatchOut& pm);
+  // boundary pass (and per-patch means) of a document gathered on the host
+  int long_pass(int64_t d, LongDoc& ld, const int64_t* doc_off, int32_t* starts, int32_t* lens,
+                int32_t* counts, const PatchOut& pm);
+  int ensure_long(int64_t L);
 };
 
 Ingest::~Ingest() {
@@ -159,8 +205,92 @@ Ingest::~Ingest() {
     for (hipEvent_t e : {s.uploaded, s.computed, s.done})
       if (e) (void)hipEventDestroy(e);
   }
+  void* lp[] = {l_H, l_N, l_C, l_starts, l_lens, l_pH, l_pN, l_pC, l_off, l_len, l_count};
+  for (void* p : lp)
+    if (p) (void)hipFree(p);
   for (hipStream_t st : {up, ks, down})
     if (st) (void)hipStreamDestroy(st);
+}
+
+void Ingest::drain() {
+  for (Slot& s : slot) {
+    if (s.busy && s.done) (void)hipEventSynchronize(s.done);
+    s.busy = false;
+    s.units.clear();
+    s.out_tokens = 0;
+  }
+}
+
+int Ingest::ensure_long(int64_t L) {
+  if (L <= long_cap) return 0;
+  // buffers in use by an earlier long pass were synchronised at its end
+  void* lp[] = {l_H, l_N, l_C, l_starts, l_lens, l_pH, l_pN, l_pC};
+  for (void* p : lp)
+    if (p) BLT_HIP_CHECK(hipFree(p));
+  l_H = l_N = l_C = l_pH = l_pN = l_pC = nullptr;
+  l_starts = l_lens = nullptr;
+  long_cap = 0;
+  BLT_HIP_CHECK(hipMalloc((void**)&l_H, (size_t)L * 4));
+  BLT_HIP_CHECK(hipMalloc((void**)&l_N, (size_t)L * 4));
+  BLT_HIP_CHECK(hipMalloc((void**)&l_C, (size_t)L * 4));
+  BLT_HIP_CHECK(hipMalloc((void**)&l_starts, (size_t)L * 4));
+  BLT_HIP_CHECK(hipMalloc((void**)&l_lens, (size_t)L * 4));
+  BLT_HIP_CHECK(hipMalloc((void**)&l_pH, (size_t)L * 4));
+  BLT_HIP_CHECK(hipMalloc((void**)&l_pN, (size_t)L * 4));
+  BLT_HIP_CHECK(hipMalloc((void**)&l_pC, (size_t)L * 4));
+  if (!l_off) {
+    BLT_HIP_CHECK(hipMalloc((void**)&l_off, 8));
+    BLT_HIP_CHECK(hipMalloc((void**)&l_len, 4));
+    BLT_HIP_CHECK(hipMalloc((void**)&l_count, 4));
+  }
+  long_cap = L;
+  return 0;
+}
+
+// The document's stitched signals are complete on the host: upload them and
+// run the same boundary / per-patch-means kernels as a one-batch document,
+// on the upload stream (which never waits on the model), then copy the
+// patches out.
+int Ingest::long_pass(int64_t d, LongDoc& ld, const int64_t* doc_off, int32_t* starts,
+                      int32_t* lens, int32_t* counts, const PatchOut& pm) {
+  const int64_t L = (int64_t)ld.H.size();
+  if (L > 0x7fffffff) return fail(BLT_ERR_SHAPE, "ingest_run: a document of 2^31 tokens or more");
+  int rc;
+  if ((rc = ensure_long(L))) return rc;
+  const int64_t zero = 0;
+  const int32_t len32 = (int32_t)L;
+  BLT_HIP_CHECK(hipMemcpyAsync(l_off, &zero, 8, hipMemcpyHostToDevice, up));
+  BLT_HIP_CHECK(hipMemcpyAsync(l_len, &len32, 4, hipMemcpyHostToDevice, up));
+  BLT_HIP_CHECK(hipMemcpyAsync(l_H, ld.H.data(), (size_t)L * 4, hipMemcpyHostToDevice, up));
+  if ((rc = launch_patch_boundaries_varlen(l_H, l_off, l_len, 1, cfg.threshold, cfg.mode, nullptr,
+                                           l_starts, l_lens, l_count, up)))
+    return rc;
+  if (pm.any()) {
+    BLT_HIP_CHECK(hipMemcpyAsync(l_N, ld.N.data(), (size_t)L * 4, hipMemcpyHostToDevice, up));
+    BLT_HIP_CHECK(hipMemcpyAsync(l_C, ld.C.data(), (size_t)L * 4, hipMemcpyHostToDevice, up));
+    if ((rc = launch_patch_means(l_H, l_N, l_C, l_starts, l_count, 1, 0, l_off, l_len, l_pH, l_pN,
+                                 l_pC, up)))
+      return rc;
+  }
+  int32_t n = 0;
+  BLT_HIP_CHECK(hipMemcpyAsync(&n, l_count, 4, hipMemcpyDeviceToHost, up));
+  BLT_HIP_CHECK(hipStreamSynchronize(up));
+  if (n < 0 || n > L) return fail(BLT_ERR_HIP, "ingest_run: bad patch count");
+  const int64_t dst = doc_off[d];
+  auto down_n = [&](void* host, const void* dev) -> int {
+    if (host && n > 0)
+      BLT_HIP_CHECK(hipMemcpyAsync(host, dev, (size_t)n * 4, hipMemcpyDeviceToHost, up));
+    return 0;
+  };
+  if ((rc = down_n(starts ? starts + dst : nullptr, l_starts))) return rc;
+  if ((rc = down_n(lens ? lens + dst : nullptr, l_lens))) return rc;
+  if ((rc = down_n(pm.ent ? pm.ent + dst : nullptr, l_pH))) return rc;
+  if ((rc = down_n(pm.prom ? pm.prom + dst : nullptr, l_pN))) return rc;
+  if ((rc = down_n(pm.coh ? pm.coh + dst : nullptr, l_pC))) return rc;
+  BLT_HIP_CHECK(hipStreamSynchronize(up));
+  if (counts) counts[d] = n;
+  ld = LongDoc{};  // release the gathered signals
+  return 0;
 }
 
 int Ingest::init(Model* model, const blt_ingest_config& c) {
@@ -217,15 +347,29 @@ int Ingest::finish(Slot& s, const int64_t* doc_off, float* ent, float* nrm, floa
   if (!s.busy) return 0;
   s.busy = false;
   BLT_HIP_CHECK(hipEventSynchronize(s.done));
-  for (size_t j = 0; j < s.docs.size(); ++j) {
-    const int64_t d = s.docs[j];
-    const int64_t L = doc_off[d + 1] - doc_off[d];
-    const int64_t src = s.h_doff[j], dst = doc_off[d];
-    const int32_t n = s.h_counts[j];
+  for (size_t j = 0; j < s.units.size(); ++j) {
+    const Unit& u = units[(size_t)s.units[j]];
+    const int64_t d = u.doc;
+    const int64_t L = u.out_len;
+    const int64_t src = s.h_doff[j], dst = doc_off[d] + u.out_lo;
     if (ent) memcpy(ent + dst, s.h_H + src, (size_t)L * 4);
     if (nrm) memcpy(nrm + dst, s.h_N + src, (size_t)L * 4);
     if (coh) memcpy(coh + dst, s.h_C + src, (size_t)L * 4);
     if (emb && s.h_E) memcpy(emb + dst * dim, s.h_E + src * dim, (size_t)(L * dim) * 4);
+    if (!u.whole) {
+      LongDoc& ld = longs[d];
+      memcpy(ld.H.data() + u.out_lo, s.h_H + src, (size_t)L * 4);
+      if (pm.any()) {
+        memcpy(ld.N.data() + u.out_lo, s.h_N + src, (size_t)L * 4);
+        memcpy(ld.C.data() + u.out_lo, s.h_C + src, (size_t)L * 4);
+      }
+      if (--ld.remaining == 0) {
+        const int rc = long_pass(d, ld, doc_off, starts, lens, counts, pm);
+        if (rc) return rc;
+      }
+      continue;
+    }
+    const int32_t n = s.h_counts[j];
     if (starts) memcpy(starts + dst, s.h_starts + src, (size_t)n * 4);
     if (lens) memcpy(lens + dst, s.h_lens + src, (size_t)n * 4);
     if (pm.ent) memcpy(pm.ent + dst, s.h_pH + src, (size_t)n * 4);
@@ -242,73 +386,107 @@ int Ingest::run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, f
   if (emb && !cfg.with_embeddings)
     return fail(BLT_ERR_INVALID, "ingest_run: embeddings asked of an ingest made without them");
   const int64_t T = cfg.row_len, B = cfg.rows;
-  std::vector<ChunkPlan> chunks;
+  // a slot still holding a batch of an earlier run that ended in an error:
+  // wait for it and drop its results (they belong to that run's arrays)
+  drain();
+  units.clear();
+  longs.clear();
+  stats = blt_ingest_stats{};
+  std::vector<ChunkPlan> chunks, sub;
   std::vector<int> order;
   std::vector<int64_t> row, col, fill(B);
-  // every document must fit an empty batch (checked before any work is queued)
+  auto fits_empty = [&](const std::vector<ChunkPlan>& c) {
+    std::fill(fill.begin(), fill.end(), 0);
+    return pack_chunks(c, fill, T, order, row, col);
+  };
+  // ---- plan: empty documents have no outputs (blt_core.rs:160-176) and
+  // never enter a batch; a document whose chunks fit an empty batch is one
+  // unit; a longer one is cut into runs of consecutive chunks that each fit
+  // (every chunk alone fits: chunk_len <= row_len) ----
   for (int64_t d = 0; d < n_docs; ++d) {
     const int64_t L = doc_off[d + 1] - doc_off[d];
     if (L < 0) return fail(BLT_ERR_SHAPE, "ingest_run: doc_offsets must be non-decreasing");
+    if (L == 0) continue;
     plan_chunks(L, cfg.chunk_len, cfg.overlap, chunks);
-    std::fill(fill.begin(), fill.end(), 0);
-    if (!pack_chunks(chunks, fill, T, order, row, col))
-      return fail(BLT_ERR_SHAPE, "ingest_run: document " + std::to_string(d) + " of " +
-                                     std::to_string(L) + " tokens does not fit one batch");
+    stats.documents += 1;
+    stats.tokens += L;
+    auto add_unit = [&](int32_t c0, int32_t c1, bool whole) {
+      Unit u{d, c0, c1, 0, 0, 0, whole};
+      u.out_lo = chunks[c0].start + chunks[c0].skip;
+      u.out_len = chunks[c1 - 1].start + chunks[c1 - 1].len - u.out_lo;
+      for (int32_t c = c0; c < c1; ++c) u.computed += chunks[c].len;
+      units.push_back(u);
+    };
+    if (fits_empty(chunks)) {
+      add_unit(0, (int32_t)chunks.size(), true);
+      continue;
+    }
+    const int32_t nc = (int32_t)chunks.size();
+    int64_t nu = 0;
+    for (int32_t c0 = 0; c0 < nc;) {
+      int32_t c1 = c0 + 1;
+      sub.assign(chunks.begin() + c0, chunks.begin() + c1);
+      while (c1 < nc) {
+        sub.push_back(chunks[c1]);
+        if (!fits_empty(sub)) break;
+        ++c1;
+      }
+      add_unit(c0, c1, false);
+      ++nu;
+      c0 = c1;
+    }
+    LongDoc& ld = longs[d];
+    ld.remaining = nu;
+    ld.H.assign((size_t)L, 0.f);
+    if (pm.any()) {
+      ld.N.assign((size_t)L, 0.f);
+      ld.C.assign((size_t)L, 0.f);
+    }
   }
   BLT_HIP_CHECK(hipSetDevice(m->device));
-  stats = blt_ingest_stats{};
-  // documents still to run, in input order; empty ones have no outputs
-  // (blt_core.rs:160-176) and never enter a batch
-  std::vector<int64_t> pending;
-  pending.reserve((size_t)n_docs);
-  for (int64_t d = 0; d < n_docs; ++d)
-    if (doc_off[d + 1] > doc_off[d]) pending.push_back(d);
-  std::vector<char> taken(pending.size(), 0);
+  std::vector<char> taken(units.size(), 0);
   size_t head = 0;
   int k = 0, rc;
-  while (head < pending.size()) {
+  while (head < units.size()) {
     Slot& s = slot[k];
     if ((rc = finish(s, doc_off, ent, nrm, coh, emb, starts, lens, counts, pm))) return rc;
     std::fill(fill.begin(), fill.end(), 0);
-    s.docs.clear();
+    s.units.clear();
     s.out_tokens = 0;
-    // ---- pack whole documents: the oldest pending one first (it always fits
-    // an empty batch), then any of the next kLookahead that still fit ----
+    // ---- pack units: the oldest pending one first (it always fits an empty
+    // batch), then any of the next kLookahead that still fit ----
     int64_t free_tokens = BT;
     size_t scanned = 0;
-    for (size_t i = head; i < pending.size() && scanned < kLookahead && free_tokens > 0; ++i) {
+    for (size_t i = head; i < units.size() && scanned < kLookahead && free_tokens > 0; ++i) {
       if (taken[i]) continue;
       ++scanned;
-      const int64_t d = pending[i];
-      const int64_t L = doc_off[d + 1] - doc_off[d];
-      if (L > free_tokens) continue;
-      plan_chunks(L, cfg.chunk_len, cfg.overlap, chunks);
-      if (!pack_chunks(chunks, fill, T, order, row, col)) continue;
+      const Unit& u = units[i];
+      if (u.computed > free_tokens) continue;
+      plan_chunks(doc_off[u.doc + 1] - doc_off[u.doc], cfg.chunk_len, cfg.overlap, chunks);
+      sub.assign(chunks.begin() + u.c0, chunks.begin() + u.c1);
+      if (!pack_chunks(sub, fill, T, order, row, col)) continue;
       taken[i] = 1;
-      const int64_t jd = (int64_t)s.docs.size();
+      const int64_t jd = (int64_t)s.units.size();
       s.h_doff[jd] = s.out_tokens;
-      s.h_dlen[jd] = (int32_t)L;
-      const int32_t* src = tokens + doc_off[d];
-      int64_t computed = 0;
-      for (size_t ci = 0; ci < chunks.size(); ++ci) {
-        const ChunkPlan& c = chunks[ci];
+      s.h_dlen[jd] = (int32_t)u.out_len;
+      const int32_t* src = tokens + doc_off[u.doc];
+      for (size_t ci = 0; ci < sub.size(); ++ci) {
+        const ChunkPlan& c = sub[ci];
         const int64_t base = row[ci] * T + col[ci];
         memcpy(s.h_tok + base, src + c.start, (size_t)c.len * 4);
-        const int32_t out0 = (int32_t)(s.out_tokens + c.start);
+        // kept output j of the chunk is document position c.start + j
+        const int32_t out0 = (int32_t)(s.out_tokens + c.start - u.out_lo);
         for (int32_t j = 0; j < c.len; ++j) {
           s.h_seg[base + j] = (int32_t)col[ci];
           s.h_dest[base + j] = j < c.skip ? -1 : out0 + j;
         }
-        computed += c.len;
       }
-      free_tokens -= computed;
-      s.out_tokens += L;
-      s.docs.push_back(d);
-      stats.documents += 1;
-      stats.tokens += L;
-      stats.tokens_computed += computed;
+      free_tokens -= u.computed;
+      s.out_tokens += u.out_len;
+      s.units.push_back((int64_t)i);
+      stats.tokens_computed += u.computed;
     }
-    while (head < pending.size() && taken[head]) ++head;
+    while (head < units.size() && taken[head]) ++head;
     // padding: every free position is its own one-token segment, output dropped
     for (int64_t r = 0; r < B; ++r)
       for (int64_t c = fill[r]; c < T; ++c) {
@@ -316,7 +494,7 @@ int Ingest::run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, f
         s.h_seg[r * T + c] = (int32_t)c;
         s.h_dest[r * T + c] = -1;
       }
-    const int64_t nd = (int64_t)s.docs.size();
+    const int64_t nd = (int64_t)s.units.size();
     stats.batches += 1;
     stats.row_tokens += BT;
     // ---- upload ----
@@ -326,7 +504,8 @@ int Ingest::run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, f
     BLT_HIP_CHECK(hipMemcpyAsync(s.d_doff, s.h_doff, (size_t)nd * 8, hipMemcpyHostToDevice, up));
     BLT_HIP_CHECK(hipMemcpyAsync(s.d_dlen, s.h_dlen, (size_t)nd * 4, hipMemcpyHostToDevice, up));
     BLT_HIP_CHECK(hipEventRecord(s.uploaded, up));
-    // ---- compute: packed forward, stitch, boundary pass ----
+    // ---- compute: packed forward, stitch, boundary pass (its results are
+    // used for whole-document units only) ----
     BLT_HIP_CHECK(hipStreamWaitEvent(ks, s.uploaded, 0));
     blt_model_outputs o{};
     o.entropies = s.d_Hp;

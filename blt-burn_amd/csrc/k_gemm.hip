@@ -69,6 +69,8 @@ int launch_gemm(const GemmArgs& a_in, hipStream_t s) {
   if ((a.xb_out != nullptr) != (a.ss_out != nullptr) ||
       (a.xb_out && (a.epi != EPI_RESID_F32 || a.ss_np * 64 != a.N || (uintptr_t)a.xb_out % 8)))
     return fail(-2, "gemm: norm partials need EPI_RESID_F32, xb_out and ss_out, ss_np = N / 64");
+  if (a.col_scale && (!a.xb_out || (uintptr_t)a.col_scale % 16))
+    return fail(-2, "gemm: col_scale scales the bf16 copy (xb_out) and must be 16-byte aligned");
 
   if ((uintptr_t)a.A % 16 != 0 || (uintptr_t)a.Bt % 16 != 0 || a.lda % 8 != 0 || a.ldb % 8 != 0)
     return fail(-2, "gemm: A and Bt rows must be 16-byte aligned (lda, ldb % 8 == 0)");

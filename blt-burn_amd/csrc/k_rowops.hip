@@ -437,15 +437,17 @@ __global__ __launch_bounds__(256) void coherence_kernel(const float* __restrict_
 // token embedding gather: x[r, :] = f32(W[clamp(tok[r]), :])   (nn::Embedding)
 // one wave per token row, 8-byte bf16 loads, 16-byte f32 stores.
 // ---------------------------------------------------------------------------
-// With xb / ss (dim % 64 == 0) the row is also copied as bf16 to xb and its
-// per-64-column sums of squares go to ss [rows, dim / 64]: the inputs of the
-// first layer's QKV GEMM, which applies the RMSNorm itself.
+// With xb / ss (dim % 64 == 0) the row, times the first layer's RMSNorm
+// weight ws (one bf16 rounding of the f32 product; ws NULL = 1), goes to xb
+// and the row's per-64-column sums of squares go to ss [rows, dim / 64]: the
+// inputs of the first layer's QKV GEMM, which applies the row factor itself.
 __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ tok,
                                                     const uint16_t* __restrict__ table,
                                                     float* __restrict__ x, int64_t rows,
                                                     int dim, int vocab,
                                                     uint16_t* __restrict__ xb,
-                                                    float* __restrict__ ss) {
+                                                    float* __restrict__ ss,
+                                                    const float* __restrict__ ws) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -459,8 +461,14 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ 
     st4(dst, e, v);
     if (xb) {
       // the 16 lanes of each 16-lane group hold one 64-column group
-      *reinterpret_cast<u32x2_t*>(xb + row * dim + e) =
-          *reinterpret_cast<const u32x2_t*>(src + e);
+      if (ws) {
+        const f32x4_t w = *reinterpret_cast<const f32x4_t*>(ws + e);
+        *reinterpret_cast<u32x2_t*>(xb + row * dim + e) =
+            u32x2_t{pack_bf16x2(v[0] * w.x, v[1] * w.y), pack_bf16x2(v[2] * w.z, v[3] * w.w)};
+      } else {
+        *reinterpret_cast<u32x2_t*>(xb + row * dim + e) =
+            *reinterpret_cast<const u32x2_t*>(src + e);
+      }
       float q = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
       q = sum16(q);
       if ((lane & 15) == 0) ss[row * (dim / 64) + e / 64] = q;
@@ -926,12 +934,13 @@ int launch_row_rstd(const float* ss, float* rstd, int64_t rows, int np, int dim,
 }
 
 int launch_embed(const int32_t* tok, const uint16_t* table, float* x, int64_t rows, int dim,
-                 int vocab, hipStream_t s, uint16_t* xb, float* ss) {
+                 int vocab, hipStream_t s, uint16_t* xb, float* ss, const float* col_scale) {
   if (rows == 0) return 0;
-  if ((xb != nullptr) != (ss != nullptr) || (xb && dim % 64))
-    return fail(BLT_ERR_SHAPE, "embed: xb and ss together, dim % 64 == 0");
+  if ((xb != nullptr) != (ss != nullptr) || (xb && dim % 64) || (col_scale && !xb) ||
+      (uintptr_t)col_scale % 16)
+    return fail(BLT_ERR_SHAPE, "embed: xb and ss together, dim % 64 == 0, 16-byte col_scale");
   hipLaunchKernelGGL(embed_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, s, tok, table, x, rows,
-                     dim, vocab, xb, ss);
+                     dim, vocab, xb, ss, col_scale);
   BLT_LAUNCH_CHECK("embed_kernel");
   return 0;
 }

@@ -9,11 +9,11 @@
 //                       land in one lane of the GEMM epilogue)
 //     w2   [L, D, F]    w2^T
 //     wout [V, D]       output^T
-//   wqkv and w13 carry their layer's RMSNorm weight folded in along K
-//   (W'[n, k] = bf16(W[n, k] * w_norm[k])); the final norm weight as f32; the
-//   RoPE cos/sin table [max_seqlen, 32, 2] f32.
+//   norm weights f32: attn_nw [L, D], ffn_nw [L, D], final_norm [D]; the RoPE
+//   cos/sin table [max_seqlen, 32, 2] f32.
 //   workspace for max_tokens rows: residual x f32 [M, D], bf16 copy of the
-//   residual (or of the final normed rows) [M, D], per-64-column sums of
+//   residual times the next projection's norm weight (or of the final normed
+//   rows) [M, D], per-64-column sums of
 //   squares of the residual f32 [M, D / 64] and the row factors 1 / (rms +
 //   eps) f32 [M] made from them, qkv bf16 [M, 3D] (q, k already
 //   rotated), attention out bf16 [M, D], FFN hidden bf16 [M, F], logits f32
@@ -24,8 +24,10 @@
 // SiLU*gate) -> W2 GEMM (+= residual, bf16 copy + sums of squares).  The
 // RMSNorm before each projection (model.rs:508-522, 758-770) is thereby split
 // between the GEMM that produces the residual and the GEMM that consumes it:
-// RMSNorm(x) W = (x * w) W / (rms(x) + eps), the per-row factor applied to
-// the consumer's accumulators.
+// RMSNorm(x) W = (x * w) W / (rms(x) + eps).  The producer's epilogue writes
+// A = bf16(x * w) (one rounding of the f32 product, as bf16(RMSNorm(x))
+// would have) and the consumer applies the per-row factor to its
+// accumulators; the projection weights stay exactly the bf16 values given.
 #include "model.hpp"
 
 #include <math.h>
@@ -116,8 +118,8 @@ int Model::read_profile(double* ms, int64_t* launches, int n) {
 
 Model::~Model() {
   for (hipEvent_t e : ev_pool) (void)hipEventDestroy(e);
-  void* ptrs[] = {emb, final_norm, wqkv, wo,   w13,  w2,     wout, rope_cs, x,
-                  a,   ss,         rstd, qkv,  attn, hbuf,   logits, ent,  norms};
+  void* ptrs[] = {emb, final_norm, attn_nw, ffn_nw, wqkv,  wo,     w13, w2,   wout, rope_cs,
+                  x,   a,          ss,      rstd,   qkv,   attn,   hbuf, logits, ent, norms};
   int prev = -1;
   (void)hipGetDevice(&prev);
   (void)hipSetDevice(device);
@@ -158,6 +160,8 @@ int Model::create(int dev, const blt_model_config& c, const blt_model_weights& w
   int rc = 0;
   rc |= dalloc(&m->emb, V * D, &tb);
   rc |= dalloc(&m->final_norm, D, &tb);
+  rc |= dalloc(&m->attn_nw, L * D, &tb);
+  rc |= dalloc(&m->ffn_nw, L * D, &tb);
   rc |= dalloc(&m->wqkv, L * 3 * D * D, &tb);
   rc |= dalloc(&m->wo, L * D * D, &tb);
   rc |= dalloc(&m->w13, L * 2 * F * D, &tb);
@@ -202,17 +206,11 @@ int Model::create(int dev, const blt_model_config& c, const blt_model_weights& w
     transpose_into(t.data(), w.output, D, V);
     if ((rc = up(m->wout, t.data(), V * D * 2))) { delete m; return rc; }
   }
-  // fold a norm weight into Bt rows: Bt[n][k] *= w[k], rounded to bf16
-  auto fold = [](uint16_t* bt, int64_t rows, int64_t K, const std::vector<float>& wn,
-                 int64_t off) {
-    for (int64_t n = 0; n < rows; ++n)
-      for (int64_t k = 0; k < K; ++k)
-        bt[n * K + k] = f32_to_bf16(bf16_to_f32(bt[n * K + k]) * wn[off + k]);
-  };
-  std::vector<float> attn_w, ffn_w;
   if (L > 0) {
-    attn_w = to_f32(w.attention_norm, L * D);
-    ffn_w = to_f32(w.ffn_norm, L * D);
+    std::vector<float> f = to_f32(w.attention_norm, L * D);
+    if ((rc = up(m->attn_nw, f.data(), L * D * 4))) { delete m; return rc; }
+    f = to_f32(w.ffn_norm, L * D);
+    if ((rc = up(m->ffn_nw, f.data(), L * D * 4))) { delete m; return rc; }
   }
   std::vector<uint16_t> tmp;
   for (int64_t l = 0; l < L; ++l) {
@@ -220,7 +218,6 @@ int Model::create(int dev, const blt_model_config& c, const blt_model_weights& w
     transpose_into(tmp.data(), w.wq + l * D * D, D, D);
     transpose_into(tmp.data() + D * D, w.wk + l * D * D, D, D);
     transpose_into(tmp.data() + 2 * D * D, w.wv + l * D * D, D, D);
-    fold(tmp.data(), 3 * D, D, attn_w, l * D);
     if ((rc = up(m->wqkv + l * 3 * D * D, tmp.data(), 3 * D * D * 2))) { delete m; return rc; }
     tmp.assign(D * D, 0);
     transpose_into(tmp.data(), w.wo + l * D * D, D, D);
@@ -235,7 +232,6 @@ int Model::create(int dev, const blt_model_config& c, const blt_model_weights& w
       const int64_t col = 32 * g + (cc & 31);
       for (int64_t k = 0; k < D; ++k) tmp[n * D + k] = src[k * F + col];
     }
-    fold(tmp.data(), 2 * F, D, ffn_w, l * D);
     if ((rc = up(m->w13 + l * 2 * F * D, tmp.data(), 2 * F * D * 2))) { delete m; return rc; }
     tmp.assign(D * F, 0);
     transpose_into(tmp.data(), w.w2 + l * F * D, F, D);
@@ -272,7 +268,7 @@ int Model::forward(const int32_t* tokens, int64_t B, int64_t T, const blt_model_
   // layer 0 reads the embedding rows as bf16 plus their sums of squares
   const bool carry = cfg.n_layers > 0;
   if ((rc = launch_embed(tokens, emb, xr, M, (int)D, (int)V, s, carry ? a : nullptr,
-                         carry ? ss : nullptr)))
+                         carry ? ss : nullptr, carry ? attn_nw : nullptr)))
     return rc;
   const int np = (int)(D / 64);
   if (carry && (rc = launch_row_rstd(ss, rstd, M, np, (int)D, cfg.norm_eps, s))) return rc;
@@ -299,7 +295,7 @@ int Model::forward(const int32_t* tokens, int64_t B, int64_t T, const blt_model_
     g = GemmArgs{};
     g.A = attn; g.Bt = wo + l * D * D; g.C = xr;
     g.M = M; g.N = D; g.K = D; g.lda = D; g.ldb = D; g.ldc = D; g.epi = EPI_RESID_F32;
-    g.xb_out = a; g.ss_out = ss; g.ss_np = np;
+    g.xb_out = a; g.ss_out = ss; g.ss_np = np; g.col_scale = ffn_nw + l * D;
     if ((rc = launch_gemm(g, s))) return rc;
     if ((rc = launch_row_rstd(ss, rstd, M, np, (int)D, cfg.norm_eps, s))) return rc;
     if ((rc = mark(BLT_STAGE_O_GEMM, s))) return rc;
@@ -314,7 +310,7 @@ int Model::forward(const int32_t* tokens, int64_t B, int64_t T, const blt_model_
     g.M = M; g.N = D; g.K = F; g.lda = F; g.ldb = F; g.ldc = D; g.epi = EPI_RESID_F32;
     const bool next = l + 1 < cfg.n_layers;  // the next layer's QKV GEMM input
     if (next) {
-      g.xb_out = a; g.ss_out = ss; g.ss_np = np;
+      g.xb_out = a; g.ss_out = ss; g.ss_np = np; g.col_scale = attn_nw + (l + 1) * D;
     }
     if ((rc = launch_gemm(g, s))) return rc;
     if (next && (rc = launch_row_rstd(ss, rstd, M, np, (int)D, cfg.norm_eps, s))) return rc;

@@ -18,6 +18,8 @@ struct Model {
   // packed weights
   uint16_t* emb = nullptr;
   float* final_norm = nullptr;
+  float* attn_nw = nullptr;  // RMSNorm weights before attention / FFN, [L, dim]
+  float* ffn_nw = nullptr;
   uint16_t* wqkv = nullptr;
   uint16_t* wo = nullptr;
   uint16_t* w13 = nullptr;

@@ -22,8 +22,10 @@ int launch_coherence(const float* nrm, const float* ent, float* out, int64_t n, 
 // factor (eps after the root) from per-64-column sums of squares
 int launch_row_rstd(const float* ss, float* rstd, int64_t rows, int np, int dim, float eps,
                     hipStream_t s);
+// (xb = bf16(row * col_scale) when col_scale is given: the first layer's norm weight)
 int launch_embed(const int32_t* tok, const uint16_t* table, float* x, int64_t rows, int dim,
-                 int vocab, hipStream_t s, uint16_t* xb = nullptr, float* ss = nullptr);
+                 int vocab, hipStream_t s, uint16_t* xb = nullptr, float* ss = nullptr,
+                 const float* col_scale = nullptr);
 int launch_rope(const uint16_t* src, uint16_t* dst, const float* cs, int64_t B, int64_t H,
                 int64_t T, int d, int64_t sb, int64_t sh, int64_t st, hipStream_t s);
 int launch_patch_boundaries(const float* H, int64_t B, int64_t T, float thr, int mode,
@@ -74,13 +76,15 @@ struct GemmArgs {
   // GEMM with xb_out set also writes bf16(new residual) to xb_out [M, ldc]
   // and, per row and 64-column group, the sum of squares of the new residual
   // to ss_out [M, ss_np] (launch_row_rstd turns those into row factors).
-  // Consumer: a GEMM with row_scale set (its A is such a bf16 residual, its Bt
-  // holds the norm weight folded in) multiplies output row r by row_scale[r]
-  // before its epilogue.
+  // col_scale (optional, [N] f32) multiplies column c of that bf16 copy only
+  // (the consumer's RMSNorm weight): xb_out = bf16(residual * col_scale).
+  // Consumer: a GEMM with row_scale set (its A is such a scaled bf16 residual)
+  // multiplies output row r by row_scale[r] before its epilogue.
   uint16_t* xb_out;
   float* ss_out;
   int ss_np;
   const float* row_scale;
+  const float* col_scale;
 };
 int launch_gemm(const GemmArgs& a, hipStream_t s);
 

@@ -107,7 +107,8 @@ class StreamingIngest:
     rows x row_len is one packed batch (it must fit the model's max_tokens);
     chunk_len / overlap / threshold come from `config` (BltConfig), the
     boundary rule from `mode` (the reference's process_bytes always applies
-    the monotonic rule, blt_core.rs:118-119, 185-186)."""
+    the monotonic rule, blt_core.rs:118-119, 185-186).  Documents may be of any
+    length: one whose chunks do not fit a batch spans several."""
 
     def __init__(self, model, config=None, rows=None, row_len=None, mode=PATCH_MONOTONIC,
                  with_embeddings=False):
@@ -167,6 +168,22 @@ class StreamingIngest:
         check(_lib.lib().blt_ingest_last_stats(self._h, ctypes.byref(st)), "ingest_last_stats")
         return {n: int(getattr(st, n)) for n, _ in IngestStats._fields_}
 
+    def stream(self, docs, segment_bytes=64 << 20, buffer_size=2, patch_means=False):
+        """Run an iterable of (sample_id, bytes) documents (or bare bytes) in
+        segments of about segment_bytes: a background thread reads and
+        tokenizes segment i + 1 (the DocumentPrefetcher role, prefetch.rs:39-149)
+        while segment i runs on the GPU.  Yields (sample_ids, tokens, IngestResult)
+        per segment, results indexed like the segment's concatenated tokens."""
+        from .prefetch import SegmentPrefetcher
+        pf = SegmentPrefetcher(docs, segment_bytes, self.config.add_bos, self.config.add_eos,
+                               buffer_size)
+        try:
+            for seg in pf:
+                yield seg.sample_ids, seg.tokens, self.run(seg.tokens, seg.token_offsets,
+                                                           patch_means=patch_means)
+        finally:
+            pf.close()
+
     def process(self, docs, sample_ids=None):
         """bytes documents -> [BltExampleWithEmbeddings] (process_bytes_with_embeddings
         for each, blt_core.rs:145-228).  pre_norm_embeddings is empty unless the
@@ -192,18 +209,31 @@ class StreamingIngest:
         return out
 
 
-def _process_one(data, sample_id, model, config, with_embeddings):
-    # one packed row per chunk of this document (rows x chunk_len must fit the
-    # model's max_tokens); the buffers live for this call only
+def ingest_for(model, config=None, with_embeddings=False, mode=PATCH_MONOTONIC):
+    """The StreamingIngest that process_bytes* use for this model and config:
+    rows of config.max_seq_len tokens, as many as the model's max_tokens holds,
+    made once and kept on the model (its pinned and device buffers are reused
+    by every later document)."""
     config = config or BltConfig()
-    n = tokenize_bytes(data, config.add_bos, config.add_eos).size
-    rows = max(1, len(plan_chunks(n, config.max_seq_len, config.chunk_overlap)))
-    if rows * config.max_seq_len > model.max_tokens:
-        raise BltError("document of %d tokens needs %d x %d model tokens; the model was made "
-                       "with max_tokens=%d" % (n, rows, config.max_seq_len, model.max_tokens))
-    ing = StreamingIngest(model, config, rows=rows, row_len=config.max_seq_len,
-                          with_embeddings=with_embeddings)
-    return ing.process([data], [sample_id])[0]
+    if config.max_seq_len > model.max_tokens:
+        raise BltError("max_seq_len %d exceeds the model's max_tokens %d"
+                       % (config.max_seq_len, model.max_tokens))
+    key = (float(config.threshold), int(config.max_seq_len), int(config.chunk_overlap),
+           bool(config.add_bos), bool(config.add_eos), int(mode), bool(with_embeddings))
+    cache = model.__dict__.setdefault("_ingest_cache", {})
+    ing = cache.get(key)
+    if ing is None:
+        ing = StreamingIngest(model, config, rows=max(1, model.max_tokens // config.max_seq_len),
+                              row_len=config.max_seq_len, mode=mode,
+                              with_embeddings=with_embeddings)
+        cache[key] = ing
+    return ing
+
+
+def _process_one(data, sample_id, model, config, with_embeddings):
+    # a document of any length: its chunks run in as many packed batches as
+    # they need (blt_core.rs:286-370 loops over them one forward at a time)
+    return ingest_for(model, config, with_embeddings).process([data], [sample_id])[0]
 
 
 def process_bytes_with_embeddings(data, sample_id, model, config=None):
@@ -223,5 +253,5 @@ def tokens_to_text(tokens):
 
 
 __all__ = ["BltConfig", "BltExample", "BltExampleWithEmbeddings", "IngestResult",
-           "StreamingIngest", "plan_chunks", "process_bytes", "process_bytes_with_embeddings",
-           "tokens_to_text", "PATCH_MONOTONIC", "PATCH_GLOBAL"]
+           "StreamingIngest", "ingest_for", "plan_chunks", "process_bytes",
+           "process_bytes_with_embeddings", "tokens_to_text", "PATCH_MONOTONIC", "PATCH_GLOBAL"]

@@ -109,6 +109,18 @@ def patch_means(entropies, norms, starts, counts, coherence=None, out=None):
             raise BltError("patch_means: coherence must match entropies")
     if out is not None:
         mH, mN, mC = out
+        if (mC is None) != (C is None):
+            raise BltError("patch_means: out must hold a coherence tensor exactly when "
+                           "coherence is given")
+        for t in (mH, mN, mC):
+            if t is None:
+                continue
+            if not isinstance(t, torch.Tensor):
+                raise TypeError("expected a torch.Tensor, got %r" % type(t))
+            if not (t.is_cuda and t.device == H.device and t.dtype == torch.float32 and
+                    tuple(t.shape) == (B, T) and t.is_contiguous()):
+                raise BltError("patch_means: out tensors must be contiguous f32 [batch, seq] "
+                               "on the entropies' device")
     else:
         mH = torch.empty((B, T), dtype=torch.float32, device=H.device)
         mN = torch.empty((B, T), dtype=torch.float32, device=H.device)

@@ -181,6 +181,40 @@ def test_ingest_config5_sample_entropy_model():
           % (off.size - 1, worst[0], worst[1]))
 
 
+def test_ingest_config5_vs_oracle_entropy_model():
+    """Config 5 at real dims (14 x 768, FFN 2048, window 512, chunks of 8192
+    with 512 overlap) against the oracle's restatement of
+    compute_all_signals_chunked + the boundary pass (blt_core.rs:178-207,
+    286-370): a document of 8704 tokens (chunks of 7680 and 1536 tokens, the
+    second starting 512 early) and the first documents of the seeded config-5
+    stream, packed together into 8192-token rows."""
+    cfg = M.entropy_model_config()
+    w = M.random_weights(cfg, 27, hidden=2048)
+    m = M.LMTransformer(cfg, w, device=0, max_tokens=2 * 8192, window=512)
+    conf = I.BltConfig(threshold=1.335, max_seq_len=8192, chunk_overlap=512)
+    ing = I.StreamingIngest(m, conf, rows=2, row_len=8192, with_embeddings=True)
+    data, off = synth.documents(synth.config_seed(5), 24 * 1024)
+    stream_lens = [int(x) for x in np.diff(off)[:4]]
+    long_doc = synth.tokens(synth.config_seed(5) + 7, (8704,))
+    toks = np.concatenate([long_doc, data[:sum(stream_lens)].astype(np.int32) + 4])
+    lens = [8704] + stream_lens
+    offs = np.zeros(len(lens) + 1, np.int64)
+    offs[1:] = np.cumsum(lens)
+    assert [c[1] for c in I.plan_chunks(8704, 8192, 512)] == [7680, 1536]
+    res = ing.run(toks.astype(np.int32), offs)
+    oc, ow = _oracle_cfg(cfg, 2048, 512), _oracle_weights(w)
+    worst = [0.0, 0.0, 0.0]
+    for d in range(len(lens)):
+        ref = oracle.process_document(oc, ow, toks[offs[d]:offs[d + 1]], 8192, 512, 1.335)
+        dH, dN = _check_doc_outputs(res, d, ref["entropies"], ref["norms"], 2e-2, 1e-2, 1.335, 0)
+        E = res.embeddings[offs[d]:offs[d + 1]]
+        rel = np.abs(E - ref["embeddings"]).max() / np.abs(ref["embeddings"]).max()
+        assert rel < 1e-2, (d, rel)
+        worst = [max(worst[0], dH), max(worst[1], dN), max(worst[2], rel)]
+    print("config-5 ingest vs oracle (%s): entropy max|d|=%.2e norms max rel=%.2e "
+          "embeddings max rel=%.2e" % (lens, *worst))
+
+
 def test_process_bytes_mirror():
     cfg = M.LMTransformerConfig(**TINY)
     w = M.random_weights(cfg, 25, hidden=256)
@@ -212,11 +246,86 @@ def test_ingest_rejects_bad_shapes():
     with pytest.raises(BltError):  # rows * row_len above the model's max_tokens
         I.StreamingIngest(m, I.BltConfig(max_seq_len=64, chunk_overlap=16), rows=4, row_len=128)
     ing = I.StreamingIngest(m, I.BltConfig(max_seq_len=64, chunk_overlap=16), rows=2, row_len=64)
-    toks, off = _docs(7, [10, 400])  # 400 tokens need 8 chunks of 64: more than 2 rows
-    with pytest.raises(BltError):
-        ing.run(toks, off)
+    with pytest.raises(BltError):  # offsets that do not end at len(tokens)
+        ing.run(np.zeros(10, np.int32) + 70, np.array([0, 5, 9], np.int64))
     res = ing.run(*_docs(8, [10, 20]))  # the handle still works after the error
     assert res.counts.size == 2 and int(res.lengths[:res.counts[0]].sum()) == 10
+
+
+def test_ingest_long_documents_vs_oracle_tiny():
+    """Documents whose chunks need more rows than one batch has (the reference
+    loops over any number of chunks, blt_core.rs:300-356): they span several
+    batches, are stitched on the host and get their boundary pass and patch
+    means once complete; short documents share the batches with them."""
+    cfg = M.LMTransformerConfig(**TINY)
+    w = M.random_weights(cfg, 31, hidden=256)
+    m = M.LMTransformer(cfg, w, device=0, max_tokens=2 * 128, window=0)
+    conf = I.BltConfig(threshold=0.3, max_seq_len=64, chunk_overlap=16)
+    ing = I.StreamingIngest(m, conf, rows=2, row_len=128, with_embeddings=True)
+    lens = [1000, 5, 0, 257, 400, 64, 2049, 3]
+    toks, off = _docs(synth.config_seed(5) + 12, lens)
+    res = ing.run(toks, off, patch_means=True)
+    st = ing.last_stats()
+    assert st["batches"] > 1 and st["tokens"] == sum(lens)
+    oc, ow = _oracle_cfg(cfg, 256, 0), _oracle_weights(w)
+    for d, L in enumerate(lens):
+        ref = oracle.process_document(oc, ow, toks[off[d]:off[d + 1]], 64, 16, 0.3)
+        _check_doc_outputs(res, d, ref["entropies"], ref["norms"], 2e-2, 1e-2, 0.3, 0)
+        if L == 0:
+            continue
+        E = res.embeddings[off[d]:off[d + 1]]
+        assert np.abs(E - ref["embeddings"]).max() < 1e-2 * np.abs(ref["embeddings"]).max()
+        H, N, C, S, Lp = res.doc(d)[:5]
+        n = S.size
+        st0 = np.zeros((1, L), np.int32)
+        st0[0, :n] = S
+        rH, rN, rC = oracle.patch_means(H[None], N[None], st0, np.array([n], np.int32), C[None])
+        starts, lengths, pH, pN, pC = res.patches(d)
+        assert np.array_equal(pH, rH[0, :n]) and np.array_equal(pN, rN[0, :n])
+        assert np.array_equal(pC, rC[0, :n])
+    # the same documents one by one give the same results
+    for d in (0, 6):
+        one = ing.run(toks[off[d]:off[d + 1]], np.array([0, lens[d]], np.int64))
+        assert np.array_equal(one.entropies, res.doc(d)[0])
+        assert np.array_equal(one.starts[:one.counts[0]], res.doc(d)[3])
+
+
+def test_ingest_long_document_entropy_model():
+    # real dims, one 8192-token row per batch: a 20000-token document is
+    # chunks of 7680, 8192 and 5152 tokens in three batches
+    cfg = M.entropy_model_config()
+    cfg.n_layers = 2
+    w = M.random_weights(cfg, 32, hidden=2048)
+    m = M.LMTransformer(cfg, w, device=0, max_tokens=8192, window=512)
+    conf = I.BltConfig(threshold=1.335, max_seq_len=8192, chunk_overlap=512)
+    ing = I.StreamingIngest(m, conf, rows=1, row_len=8192)
+    toks, off = _docs(synth.config_seed(5) + 13, [20000, 300])
+    assert [c[1] for c in I.plan_chunks(20000, 8192, 512)] == [7680, 8192, 5152]
+    res = ing.run(toks, off)
+    assert ing.last_stats()["batches"] == 3
+    for d in range(2):
+        H, N = _direct_chunks(m, toks[off[d]:off[d + 1]], 8192, 512)
+        _check_doc_outputs(res, d, H, N, 5e-3, 5e-3, 1.335, 0)
+
+
+def test_process_bytes_long_document_reuses_ingest():
+    cfg = M.LMTransformerConfig(**TINY)
+    w = M.random_weights(cfg, 33, hidden=256)
+    m = M.LMTransformer(cfg, w, device=0, max_tokens=256, window=0)
+    conf = I.BltConfig(max_seq_len=64, chunk_overlap=16)
+    data = (synth.tokens(synth.config_seed(5) + 14, (3000,)) - 4).astype(np.uint8).tobytes()
+    ex = I.process_bytes_with_embeddings(data, "long", m, conf)
+    toks = ex.core.tokens
+    assert toks.size > 256 and int(ex.core.patch_lengths.sum()) == toks.size
+    ref = oracle.process_document(_oracle_cfg(cfg, 256, 0), _oracle_weights(w), toks, 64, 16,
+                                  conf.threshold)
+    assert np.abs(ex.core.entropies - ref["entropies"]).max() < 2e-2
+    np.testing.assert_array_equal(ex.patch_indices, oracle.patch_indices(
+        oracle.patch_mask(ex.core.entropies[None], conf.threshold, 0))[0])
+    ing = I.ingest_for(m, conf, with_embeddings=True)
+    assert I.ingest_for(m, conf, with_embeddings=True) is ing
+    ex2 = I.process_bytes_with_embeddings(data, "long", m, conf)
+    assert np.array_equal(ex2.core.entropies, ex.core.entropies)
 
 
 def test_ingest_patch_means_bit_exact():

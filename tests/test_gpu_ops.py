@@ -428,3 +428,59 @@ def test_gemm_persistent_many_tiles_odd_k_tiles(K):
     u = y.view(M, N // 64, 2, 32)[:, :, 1, :].reshape(M, N // 2)
     ref = torch.nn.functional.silu(g) * u
     assert (h.float() - ref).abs().max().item() <= tol(ref)
+
+
+# ---------------------------------------------------------------- N % 128 == 64 column bound
+def _gemm_epi_ld(a, bt, buf, ldc, epi, rope_cols=0, seq_len=1, cs=None):
+    M, K = a.shape
+    N = bt.shape[0]
+    _lib.check(_lib.lib().blt_gemm_bf16_epilogue(
+        a.data_ptr(), bt.data_ptr(), buf.data_ptr(), M, N, K, K, K, ldc, epi, 0, rope_cols,
+        seq_len, cs.data_ptr() if cs is not None else 0,
+        torch.cuda.current_stream().cuda_stream), "gemm_epilogue")
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("N,pad", [(192, 0), (192, 64), (576, 0), (320, 64)])
+def test_gemm_pair_epilogues_n_mod_128_is_64(N, pad):
+    """N % 256 != 0 takes the 128 x 128 register-staged kernel; with N % 128 ==
+    64 its last N tile overhangs N by 64 columns.  The RoPE and SiLU*gate pair
+    epilogues must write nothing there: a sentinel-filled row padding (pad)
+    and a guard region after the last row stay untouched."""
+    M, K = 300, 256
+    torch.manual_seed(N + pad)
+    a = torch.randn(M, K, device=DEV).to(torch.bfloat16)
+    bt = (0.1 * torch.randn(N, K, device=DEV)).to(torch.bfloat16)
+    y = a.float() @ bt.float().t()
+    sentinel = torch.tensor(-12345.0, dtype=torch.bfloat16)
+    guard = 4096
+    T = 100
+    cs = torch.from_numpy(oracle.rope_table(64, T, 10000.0)).to(DEV)
+    for epi in (_lib.EPI_QKV_ROPE, _lib.EPI_SILU_GATE):
+        width = N if epi == _lib.EPI_QKV_ROPE else N // 2
+        ldc = width + pad
+        buf = torch.full((M * ldc + guard,), sentinel.item(), device=DEV, dtype=torch.bfloat16)
+        rope_cols = (N // 64 // 2) * 64 if epi == _lib.EPI_QKV_ROPE else 0
+        _gemm_epi_ld(a, bt, buf, ldc, epi, rope_cols=rope_cols, seq_len=T, cs=cs)
+        c = buf[:M * ldc].view(M, ldc)
+        assert torch.all(buf[M * ldc:] == sentinel), "wrote past the last row"
+        if pad:
+            assert torch.all(c[:, width:] == sentinel), "wrote into the row padding"
+        out = c[:, :width].float()
+        if epi == _lib.EPI_SILU_GATE:
+            g = y.view(M, N // 64, 2, 32)[:, :, 0, :].reshape(M, N // 2)
+            u = y.view(M, N // 64, 2, 32)[:, :, 1, :].reshape(M, N // 2)
+            ref = torch.nn.functional.silu(g) * u
+        else:
+            yy = y.cpu().numpy()
+            ref = yy.copy()
+            pos = np.arange(M) % T
+            q = yy[:, :rope_cols].reshape(M, rope_cols // 64, 64)
+            cos = cs.cpu().numpy()[pos, :, 0][:, None, :]
+            sin = cs.cpu().numpy()[pos, :, 1][:, None, :]
+            x1, x2 = q[..., :32], q[..., 32:]
+            ref[:, :rope_cols] = np.concatenate([x1 * cos - x2 * sin, x1 * sin + x2 * cos],
+                                                -1).reshape(M, rope_cols)
+            ref = torch.from_numpy(ref).to(DEV)
+        err = (out - ref).abs().max().item()
+        assert err <= 2 ** -7 * ref.abs().max().item() + 1e-3, (epi, err)

@@ -104,3 +104,27 @@ def test_device_bit_exact_vs_oracle():
     e = torch.empty(0, 5, device="cuda")
     patcher.patch_means(e, e, torch.empty(0, 5, dtype=torch.int32, device="cuda"),
                         torch.empty(0, dtype=torch.int32, device="cuda"))
+
+
+@pytest.mark.gpu
+def test_device_rejects_bad_out_tensors():
+    import torch
+    from blt_burn_amd import BltError, patcher
+    Hd = torch.rand(2, 64, device="cuda")
+    _, s, _, c = patcher.patch_boundaries(Hd, 0.1)
+    good = torch.empty(2, 64, device="cuda")
+    bad = [torch.empty(2, 63, device="cuda"),                   # too small
+           torch.empty(2, 64, device="cuda", dtype=torch.float64),
+           torch.empty(64, 2, device="cuda").t(),               # not contiguous
+           torch.empty(2, 64)]                                  # host memory
+    for t in bad:
+        with pytest.raises(BltError):
+            patcher.patch_means(Hd, Hd, s, c, out=(t, good, None))
+        with pytest.raises(BltError):
+            patcher.patch_means(Hd, Hd, s, c, out=(good, t, None))
+    with pytest.raises(BltError):  # a coherence output without coherence input
+        patcher.patch_means(Hd, Hd, s, c, out=(good, good.clone(), good.clone()))
+    with pytest.raises(BltError):  # coherence given, no output for it
+        patcher.patch_means(Hd, Hd, s, c, Hd, out=(good, good.clone(), None))
+    mH, mN, _ = patcher.patch_means(Hd, Hd, s, c, out=(good, good.clone(), None))
+    assert mH is good
