@@ -60,7 +60,7 @@ def _dispatch_stages(names, layers):
             out.append("rmsnorm")
         elif "entropy_" in n and "_kernel" in n:
             out.append("entropy")
-        elif "patch_boundary_kernel" in n:
+        elif "patch_boundary_kernel" in n or "patch_tile_kernel" in n:
             out.append("patch_boundaries")
         elif "embed_kernel" in n:
             out.append("embed")
@@ -380,36 +380,59 @@ def _cpu_cores():
     return cores
 
 
+def _graph_launch_ms(fn, launches, replays=10):
+    """Mean ms per call of fn() when `launches` calls are replayed back to back
+    from a HIP graph (no host gaps between them), HIP events on the stream
+    the graph is replayed on."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(launches):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (replays * launches)
+
+
 def bench_config1(args):
-    """Config 1: fused entropy over f32 logits [4, 8192, 260] ~ N(0, 2) and the
-    patch-boundary passes (global H > 1.33, monotonic dH > 0.2), inputs in HBM.
-    value = positions per second for the whole step (entropy + both passes);
-    roofline = the entropy kernel's HBM rate (1040 B read + 4 B written per
-    position) against 8 TB/s."""
+    """Config 1: softmax entropy over f32 logits [4, 8192, 260] ~ N(0, 2) and the
+    global (H > 1.33) and monotonic (dH > 0.2) boundaries with their start
+    indices and lengths, inputs in HBM.  One call of entropy_patch_boundaries
+    per step: a flags kernel reads the logits once and writes the entropies,
+    both masks and per-tile counts, a compaction kernel writes the starts and
+    lengths.  value = positions per second of the eager step; roofline = the
+    call's HBM rate (its algorithmic bytes over its mean duration, calls
+    replayed back to back from a HIP graph) against 8 TB/s."""
     import numpy as np
     import torch
-    from blt_burn_amd import fused_ops, patcher, synth
+    from blt_burn_amd import patcher, synth
     steps = args.steps or 50
     B, T, V = 4, 8192, 260
     logits_np = synth.normal_f32(synth.config_seed(1), (B, T, V), 0.0, 2.0)
     logits = torch.from_numpy(logits_np).cuda()
+    rules = [(patcher.PATCH_GLOBAL, 1.33), (patcher.PATCH_MONOTONIC, 0.2)]
     bnd = [tuple(torch.empty(s, dtype=torch.int32, device="cuda")
                  for s in ((B, T), (B, T), (B, T), (B,))) for _ in range(2)]
-    Hbuf = {}
+    Hbuf = torch.empty((B, T), dtype=torch.float32, device="cuda")
 
     def step():
-        H = fused_ops.fused_entropy(logits, V)
-        Hbuf["H"] = H
-        patcher.patch_boundaries(H, 1.33, patcher.PATCH_GLOBAL, out=bnd[0])
-        patcher.patch_boundaries(H, 0.2, patcher.PATCH_MONOTONIC, out=bnd[1])
+        patcher.entropy_patch_boundaries(logits, rules, out=bnd, entropies=Hbuf)
 
     ms = _timed(step, steps, args.warmup)
-    ms_ent = _timed(lambda: fused_ops.fused_entropy(logits, V), steps, args.warmup)
-    ms_bnd = _timed(lambda: patcher.patch_boundaries(Hbuf["H"], 0.2, patcher.PATCH_MONOTONIC,
-                                                     out=bnd[1]), steps, args.warmup)
+    ms_k = _graph_launch_ms(step, 20)
     n = B * T
-    ent_bytes = n * (V * 4 + 4)
-    gbs = ent_bytes / (ms_ent * 1e-3) / 1e9
+    counts = [int(bnd[r][3].sum()) for r in range(2)]
+    # logits read, entropies written, both masks, the starts and lengths written
+    k_bytes = n * (V * 4 + 4) + 2 * n * 4 + 8 * sum(counts)
+    gbs = k_bytes / (ms_k * 1e-3) / 1e9
     result = {
         "metric": "positions/sec through fused entropy + global and monotonic patch boundaries "
                   "(config 1, f32 logits [4, 8192, 260])",
@@ -417,14 +440,17 @@ def bench_config1(args):
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic: logits ~ N(0, 2.0), seed %d" % synth.config_seed(1),
-        "config": {"workload": "config1: fused_entropy + patch boundaries (global 1.33, "
-                               "monotonic 0.2)", "batch": B, "seq_len": T, "vocab": V},
-        "roofline": _with_achievable({"bound": "hbm", "kernel": "entropy_tail_kernel",
+        "config": {"workload": "config1: entropy + global (1.33) and monotonic (0.2) patch "
+                               "boundaries, starts and lengths, one pass",
+                   "batch": B, "seq_len": T, "vocab": V},
+        "roofline": _with_achievable({"bound": "hbm",
+                                      "kernel": "entropy_flags_kernel<1, 1, 16> + "
+                                                "patch_compact_kernel<1> (one call)",
                                       "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                                       "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                                      "traffic": None, "launch_ms": round(ms_ent, 4),
-                                      "bytes_per_launch": ent_bytes}),
-        "boundary_pass_ms": round(ms_bnd, 4),
+                                      "traffic": None, "launch_ms": round(ms_k, 5),
+                                      "bytes_per_launch": k_bytes}),
+        "starts": {"global": counts[0], "monotonic": counts[1]},
         "cpu_baseline": None,
     }
     if not args.no_cpu:
@@ -441,7 +467,7 @@ def bench_config1(args):
             c1 = time.perf_counter()
             if c1 - c0 > 2.0:
                 break
-        Hg = Hbuf["H"].cpu().numpy()[:Bs]
+        Hg = Hbuf.cpu().numpy()[:Bs]
         m_g = bnd[1][0].cpu().numpy()[:Bs]
         result["cpu_baseline"] = {
             "value": round(reps * Bs * T / (c1 - c0), 1), "unit": "positions/s",

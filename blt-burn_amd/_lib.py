@@ -44,6 +44,10 @@ EXPORTS = {
                                      c_vp]),
     "blt_patch_means": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp,
                                 c_vp]),
+    "blt_patch_workspace_bytes": (c_i64, [c_i64, c_i64, c_i32]),
+    "blt_patch_boundaries_rules": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_vp, c_vp, c_i64, c_vp]),
+    "blt_entropy_patch_boundaries": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_vp, c_i32, c_vp, c_vp,
+                                             c_i64, c_vp]),
     "blt_model_create": (c_i32, [c_i32, c_vp, c_vp, c_i64, ctypes.POINTER(c_vp)]),
     "blt_model_destroy": (c_i32, [c_vp]),
     "blt_model_device_bytes": (c_i64, [c_vp]),
@@ -96,6 +100,12 @@ OUTPUT_FIELDS = ("logits", "pre_norm_embeddings", "embedding_norms", "entropies"
 
 class ModelOutputs(ctypes.Structure):
     _fields_ = [(n, c_vp) for n in OUTPUT_FIELDS]
+
+
+class PatchRule(ctypes.Structure):
+    """blt_patch_rule."""
+    _fields_ = [("mode", c_i32), ("threshold", c_f32), ("mask", c_vp), ("starts", c_vp),
+                ("lengths", c_vp), ("count", c_vp)]
 
 
 class IngestStats(ctypes.Structure):

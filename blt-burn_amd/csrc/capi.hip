@@ -325,6 +325,23 @@ int blt_patch_means(const float* entropies, const float* norms, const float* coh
                             mean_entropy, mean_prominence, mean_coherence, STREAM(stream));
 }
 
+int64_t blt_patch_workspace_bytes(int64_t B, int64_t T, int32_t n_rules) {
+  return patch_workspace_bytes(B, T, n_rules);
+}
+
+int blt_patch_boundaries_rules(const float* H, int64_t B, int64_t T, int32_t n_rules,
+                               const blt_patch_rule* rules, void* workspace,
+                               int64_t workspace_bytes, blt_stream_t stream) {
+  return launch_patch_rules(H, B, T, n_rules, rules, workspace, workspace_bytes, STREAM(stream));
+}
+
+int blt_entropy_patch_boundaries(const float* logits, int64_t B, int64_t T, int32_t vocab,
+                                 float* entropies, int32_t n_rules, const blt_patch_rule* rules,
+                                 void* workspace, int64_t workspace_bytes, blt_stream_t stream) {
+  return launch_entropy_patch(logits, B, T, vocab, entropies, n_rules, rules, workspace,
+                              workspace_bytes, STREAM(stream));
+}
+
 // ---- model -------------------------------------------------------------------
 int blt_model_create(int32_t device, const blt_model_config* cfg, const blt_model_weights* w,
                      int64_t max_tokens, blt_model** out) {

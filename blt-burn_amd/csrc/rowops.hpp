@@ -1,5 +1,6 @@
 // Host launchers of the kernels (each returns 0 or a negative blt_status).
 #pragma once
+#include "../../include/blt_hip.h"
 #include "common.hpp"
 
 namespace blt {
@@ -46,6 +47,17 @@ int launch_patch_boundaries_varlen(const float* H, const int64_t* row_off, const
                                    int64_t rows, float thr, int mode, int32_t* mask,
                                    int32_t* starts, int32_t* lengths, int32_t* count,
                                    hipStream_t s);
+
+// k_patch.hip: boundary rules over many blocks per row; ws = a workspace of
+// patch_workspace_bytes (no initialisation needed)
+int64_t patch_workspace_bytes(int64_t B, int64_t T, int n_rules);
+int launch_patch_rules(const float* H, int64_t B, int64_t T, int n_rules,
+                       const blt_patch_rule* rules, void* ws, int64_t ws_bytes, hipStream_t s);
+// softmax entropy of logits [B * T, vocab] (into H_out, may be NULL when the
+// vocab has a fused variant) and the rules in one pass
+int launch_entropy_patch(const float* logits, int64_t B, int64_t T, int vocab, float* H_out,
+                         int n_rules, const blt_patch_rule* rules, void* ws, int64_t ws_bytes,
+                         hipStream_t s);
 
 // k_gemm.hip -----------------------------------------------------------------
 // C[M, N] = A[M, K] . Bt[N, K]^T with bf16 operands and f32 accumulation; the

@@ -1,8 +1,16 @@
 """Patcher API of the reference (src/patcher.rs) on the GPU.
 
 entropy / patch_start_mask_from_entropy_with_monotonicity keep the reference's
-signatures; the device kernel behind them also compacts start indices and
+signatures; the device pass behind them also compacts start indices and
 lengths (patch_boundaries), so patch_start_indices_cpu only copies results.
+
+The pass runs many blocks per row and passes per-tile counts and flag words
+between its kernels through a per-device workspace, so calls on one device
+must be stream-ordered: torch's current stream of one thread, or streams the
+caller orders.  Two rules (e.g. the global and the
+monotonic mask) can share one read of the entropies (patch_boundaries_rules),
+and entropy_patch_boundaries computes the entropies and the rules in one pass
+over the logits.
 """
 import torch
 
@@ -12,7 +20,8 @@ from ._torch import contiguous, require_cuda, stream_ptr
 from .fused_ops import fused_entropy
 
 __all__ = ["entropy", "patch_start_mask_from_entropy_with_monotonicity",
-           "patch_start_mask_global", "patch_boundaries", "patch_start_indices_cpu",
+           "patch_start_mask_global", "patch_boundaries", "patch_boundaries_rules",
+           "entropy_patch_boundaries", "patch_start_indices_cpu",
            "patch_lengths_from_start_indices", "patch_means", "PATCH_MONOTONIC",
            "PATCH_GLOBAL"]
 
@@ -22,35 +31,112 @@ def entropy(scores):
     return fused_entropy(scores, scores.shape[-1])
 
 
+_WORKSPACE = {}  # device index -> uint8 tensor passed between the pass's kernels
+
+
+def _workspace(device, nbytes):
+    """The device's boundary-pass workspace, grown when a call needs more;
+    growing it inside a HIP graph capture is refused (run the call once
+    eagerly first, as the capture then reuses it)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _WORKSPACE.get(idx)
+    if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise BltError("the patch workspace must exist before graph capture: run the "
+                           "boundary pass once eagerly first")
+        ws = torch.empty(max(int(nbytes), 1 << 16), dtype=torch.uint8,
+                         device=torch.device("cuda", idx))
+        _WORKSPACE[idx] = ws
+    return ws
+
+
+def _rule_outputs(B, T, device, out):
+    i32 = torch.int32
+    if out is not None:
+        mask, starts, lengths, counts = out
+        for t, shp in ((mask, (B, T)), (starts, (B, T)), (lengths, (B, T)), (counts, (B,))):
+            require_cuda(t)
+            if not (t.dtype == i32 and tuple(t.shape) == shp and t.is_contiguous() and
+                    t.device == device):
+                raise BltError("patch boundaries: out tensors must be contiguous int32 "
+                               "[batch, seq] x3 and [batch] on the entropies' device")
+        return tuple(out)
+    return (torch.empty((B, T), dtype=i32, device=device),
+            torch.empty((B, T), dtype=i32, device=device),
+            torch.empty((B, T), dtype=i32, device=device),
+            torch.empty((B,), dtype=i32, device=device))
+
+
+def _rules_struct(rules, outs):
+    if not 1 <= len(rules) <= 2:
+        raise BltError("one or two boundary rules per pass")
+    arr = (_lib.PatchRule * len(rules))()
+    for r, ((mode, thr), (mask, starts, lengths, counts)) in enumerate(zip(rules, outs)):
+        arr[r] = _lib.PatchRule(int(mode), float(thr), mask.data_ptr(), starts.data_ptr(),
+                                lengths.data_ptr(), counts.data_ptr())
+    return arr
+
+
+def patch_boundaries_rules(entropies, rules, out=None):
+    """One or two boundary rules over entropies [batch, seq] f32 in one read
+    (patcher.rs:80-164 once per rule).  rules: [(mode, threshold), ...].
+    Returns one (mask, starts, lengths, counts) per rule, laid out as
+    patch_boundaries returns them; `out` may pass them preallocated."""
+    require_cuda(entropies)
+    if entropies.dim() != 2:
+        raise BltError("patch_boundaries expects [batch, seq]")
+    H = contiguous(entropies if entropies.dtype == torch.float32 else entropies.to(torch.float32))
+    B, T = H.shape
+    rules = list(rules)
+    outs = [_rule_outputs(B, T, H.device, out[r] if out is not None else None)
+            for r in range(len(rules))]
+    arr = _rules_struct(rules, outs)
+    L = _lib.lib()
+    nbytes = L.blt_patch_workspace_bytes(B, T, len(rules))
+    ws = _workspace(H.device, nbytes)
+    check(L.blt_patch_boundaries_rules(H.data_ptr(), B, T, len(rules), arr, ws.data_ptr(),
+                                       ws.numel(), stream_ptr(H.device)), "patch_boundaries")
+    return outs
+
+
+def entropy_patch_boundaries(logits, rules, out=None, entropies=None):
+    """patcher::entropy (patcher.rs:15-22) and then the boundary rules, in one
+    pass over logits [batch, seq, vocab] f32.  Returns (entropies [batch, seq]
+    f32, [(mask, starts, lengths, counts) per rule])."""
+    require_cuda(logits)
+    if logits.dim() != 3 or logits.dtype != torch.float32:
+        raise BltError("entropy_patch_boundaries expects f32 logits [batch, seq, vocab]")
+    x = contiguous(logits)
+    B, T, V = x.shape
+    if entropies is None:
+        entropies = torch.empty((B, T), dtype=torch.float32, device=x.device)
+    else:
+        require_cuda(entropies)
+        if not (entropies.dtype == torch.float32 and tuple(entropies.shape) == (B, T) and
+                entropies.is_contiguous() and entropies.device == x.device):
+            raise BltError("entropy_patch_boundaries: entropies out must be contiguous f32 "
+                           "[batch, seq] on the logits' device")
+    rules = list(rules)
+    outs = [_rule_outputs(B, T, x.device, out[r] if out is not None else None)
+            for r in range(len(rules))]
+    arr = _rules_struct(rules, outs)
+    L = _lib.lib()
+    nbytes = L.blt_patch_workspace_bytes(B, T, len(rules))
+    ws = _workspace(x.device, nbytes)
+    check(L.blt_entropy_patch_boundaries(x.data_ptr(), B, T, V, entropies.data_ptr(), len(rules),
+                                         arr, ws.data_ptr(), ws.numel(), stream_ptr(x.device)),
+          "entropy_patch_boundaries")
+    return entropies, outs
+
+
 def patch_boundaries(entropies, threshold, mode=PATCH_MONOTONIC, out=None):
     """Device pass over entropies [batch, seq] f32.  Returns (mask, starts, lengths,
     counts): mask [B, T] int32, starts/lengths [B, T] int32 with counts[b] valid
     entries per row, counts [B] int32.  mode PATCH_MONOTONIC: patcher.rs:80-118;
     PATCH_GLOBAL: same layout with H[t] > threshold.  `out` may pass the four
     result tensors preallocated (reused as is)."""
-    require_cuda(entropies)
-    if entropies.dim() != 2:
-        raise BltError("patch_boundaries expects [batch, seq]")
-    H = contiguous(entropies if entropies.dtype == torch.float32 else entropies.to(torch.float32))
-    B, T = H.shape
-    if out is not None:
-        mask, starts, lengths, counts = out
-        i32 = torch.int32
-        for t, shp in ((mask, (B, T)), (starts, (B, T)), (lengths, (B, T)), (counts, (B,))):
-            if not (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == i32 and
-                    t.shape == shp and t.is_contiguous()):
-                require_cuda(t)
-                raise BltError("patch_boundaries: out tensors must be contiguous int32")
-    else:
-        mask = torch.empty((B, T), dtype=torch.int32, device=H.device)
-        starts = torch.empty((B, T), dtype=torch.int32, device=H.device)
-        lengths = torch.empty((B, T), dtype=torch.int32, device=H.device)
-        counts = torch.empty((B,), dtype=torch.int32, device=H.device)
-    check(_lib.lib().blt_patch_boundaries(H.data_ptr(), B, T, float(threshold), mode,
-                                          mask.data_ptr(), starts.data_ptr(), lengths.data_ptr(),
-                                          counts.data_ptr(), stream_ptr(H.device)),
-          "patch_boundaries")
-    return mask, starts, lengths, counts
+    return patch_boundaries_rules(entropies, [(mode, threshold)],
+                                  out=[out] if out is not None else None)[0]
 
 
 def patch_start_mask_from_entropy_with_monotonicity(entropies, threshold):

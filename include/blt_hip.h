@@ -140,6 +140,42 @@ int blt_patch_boundaries(const float* H, int64_t B, int64_t T, float thr, int32_
                          int32_t* mask, int32_t* starts, int32_t* lengths, int32_t* count,
                          blt_stream_t stream);
 
+/* One boundary rule and its outputs, laid out as blt_patch_boundaries writes
+ * them (each output may be NULL; lengths needs starts). */
+typedef struct blt_patch_rule {
+  int32_t mode;      /* blt_patch_mode */
+  float threshold;   /* delta (monotonic) or theta (global), compared in f32 */
+  int32_t* mask;     /* [B, T] */
+  int32_t* starts;   /* [B, T], count[b] valid entries in row b */
+  int32_t* lengths;  /* [B, T], count[b] valid entries in row b */
+  int32_t* count;    /* [B] */
+} blt_patch_rule;
+
+/* Device bytes of the workspace of blt_patch_boundaries_rules and
+ * blt_entropy_patch_boundaries for [B, T] and n_rules (1 or 2) rules. */
+int64_t blt_patch_workspace_bytes(int64_t B, int64_t T, int32_t n_rules);
+
+/* The same outputs as blt_patch_boundaries (patcher.rs:80-164), for one or two
+ * rules from one read of H (the reference calls the mask function once per
+ * rule), with many blocks per row (per-tile flags, then per-tile compaction).
+ * workspace: device memory of at least blt_patch_workspace_bytes(B, T, n_rules)
+ * bytes, 16-byte aligned, holding per-tile counts and flag words between the
+ * call's kernels; it needs no initialisation and keeps nothing between calls,
+ * but calls that share one must be stream-ordered. */
+int blt_patch_boundaries_rules(const float* H, int64_t B, int64_t T, int32_t n_rules,
+                               const blt_patch_rule* rules, void* workspace,
+                               int64_t workspace_bytes, blt_stream_t stream);
+
+/* patcher::entropy (patcher.rs:15-22; NdArray form 38-63) followed by the
+ * rules of blt_patch_boundaries_rules, in one pass over the logits when
+ * vocab % 4 == 0, vocab < 1280 and the rows are 16-byte aligned (otherwise
+ * the entropy kernel and the rule pass run one after the other).
+ * logits [B, T, vocab] f32; entropies [B, T] f32 out (may be NULL on the
+ * one-pass path).  Workspace as for blt_patch_boundaries_rules. */
+int blt_entropy_patch_boundaries(const float* logits, int64_t B, int64_t T, int32_t vocab,
+                                 float* entropies, int32_t n_rules, const blt_patch_rule* rules,
+                                 void* workspace, int64_t workspace_bytes, blt_stream_t stream);
+
 /* Per-patch means over the patches blt_patch_boundaries found: for row b and
  * patch p < count[b], the patch covers [starts[b*T + p], starts[b*T + p + 1]) (the
  * last to T) and

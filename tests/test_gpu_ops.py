@@ -211,6 +211,102 @@ def test_patch_boundaries_config1():
     np.testing.assert_array_equal(m, oracle.patch_mask(H, 0.2, 0))
 
 
+def _check_rule_outputs(H, thr, mode, outs):
+    mask, starts, lengths, counts = (t.cpu().numpy() for t in outs)
+    ref_mask = oracle.patch_mask(H, thr, mode)
+    np.testing.assert_array_equal(mask, ref_mask)
+    ref_starts = oracle.patch_indices(ref_mask)
+    ref_len = oracle.patch_lengths(ref_starts, H.shape[1])
+    for b in range(H.shape[0]):
+        assert counts[b] == len(ref_starts[b])
+        assert starts[b, :counts[b]].tolist() == ref_starts[b]
+        assert lengths[b, :counts[b]].tolist() == ref_len[b]
+
+
+# shapes around the 64-position (fused) and 1024-position tiles, rows of more
+# than 4096 tiles (the scan kernel), and T = 0, 1, 2
+RULE_SHAPES = [(1, 0), (3, 1), (2, 2), (2, 3), (1, 63), (1, 64), (1, 65), (2, 1023), (2, 1024),
+               (2, 1025), (4, 8191), (4, 8192), (2, 8193), (1, 20000), (16, 8192), (1, 70000),
+               (3, 66 * 1024 + 5), (1, 4096 * 1024 + 3000)]
+
+
+@pytest.mark.parametrize("B,T", RULE_SHAPES)
+def test_patch_rules_two_rules_one_read(B, T):
+    # monotonic and global rules from one read of H, bit-exact vs the oracle
+    H = np.abs(synth.normal_f32(31 + T, (B, T), 1.4, 0.6))
+    rules = [(patcher.PATCH_MONOTONIC, 0.2), (patcher.PATCH_GLOBAL, 1.33)]
+    outs = patcher.patch_boundaries_rules(cuda(H), rules)
+    for (mode, thr), o in zip(rules, outs):
+        _check_rule_outputs(H, thr, mode, o)
+
+
+def test_patch_rules_threshold_edges():
+    # H on a 0.25 grid, so every f32 difference is exactly 0 or 0.25: a
+    # difference equal to the threshold starts no patch, the next f32 below
+    # it as threshold makes every step a start; the global rule sees the same
+    # values against a threshold equal to one of them
+    k = np.cumsum(synth.normal_f32(7, 5000) > 0.3).astype(np.float32)
+    H = np.stack([0.25 * k, 0.25 * k[::-1].copy()]).astype(np.float32)
+    below = float(np.nextafter(np.float32(0.25), np.float32(0)))
+    for thr in (0.25, below):
+        outs = patcher.patch_boundaries_rules(cuda(H), [(0, thr), (1, 10.0)])
+        _check_rule_outputs(H, thr, 0, outs[0])
+        _check_rule_outputs(H, 10.0, 1, outs[1])
+        n_up = int((np.diff(H[0]) == 0.25)[1:].sum())
+        assert int(outs[0][3][0]) == 2 + (0 if thr == 0.25 else n_up)
+
+
+@pytest.mark.parametrize("V", [260, 256, 100, 4, 1024, 1000, 13, 1280])
+@pytest.mark.parametrize("B,T", [(4, 8192), (2, 1025), (1, 1), (2, 0), (1, 9000), (2, 300000)])
+def test_entropy_patch_boundaries_vs_oracle(V, B, T):
+    # entropies (1e-4 abs vs the oracle, identical to fused_entropy) and both
+    # rules bit-exact on those entropies; V 13 and 1280 take the two-kernel path
+    if B * T * V > 40_000_000:
+        T = 40_000_000 // (B * V)
+    x = synth.normal_f32(41 + V + T, (B, T, V), 0.0, 2.0)
+    xs = x * np.linspace(0.2, 4.0, max(T, 1), dtype=np.float32)[None, :T, None]
+    rules = [(patcher.PATCH_GLOBAL, 1.33 if V > 8 else 0.5), (patcher.PATCH_MONOTONIC, 0.2)]
+    Hd, outs = patcher.entropy_patch_boundaries(cuda(xs), rules)
+    H = Hd.cpu().numpy()
+    if T > 0:
+        np.testing.assert_allclose(H, oracle.entropy(xs), atol=1e-4, rtol=0)
+        assert torch.equal(Hd, F.fused_entropy(cuda(xs), V))
+    for (mode, thr), o in zip(rules, outs):
+        _check_rule_outputs(H, thr, mode, o)
+
+
+def test_patch_rules_workspace_reused_across_sizes():
+    # one workspace through calls of growing and shrinking size, one and two
+    # rules, both kernels: every call matches the oracle
+    for k, (B, T, n) in enumerate([(4, 8192, 2), (1, 100, 1), (2, 70000, 2), (3, 5, 1),
+                                   (16, 8192, 1), (1, 65, 2)]):
+        H = np.abs(synth.normal_f32(90 + k, (B, T), 1.4, 0.6))
+        rules = [(patcher.PATCH_MONOTONIC, 0.2), (patcher.PATCH_GLOBAL, 1.33)][:n]
+        outs = patcher.patch_boundaries_rules(cuda(H), rules)
+        for (mode, thr), o in zip(rules, outs):
+            _check_rule_outputs(H, thr, mode, o)
+        x = synth.normal_f32(190 + k, (B, min(T, 3000), 260), 0.0, 2.0)
+        Hd, outs = patcher.entropy_patch_boundaries(cuda(x), rules)
+        for (mode, thr), o in zip(rules, outs):
+            _check_rule_outputs(Hd.cpu().numpy(), thr, mode, o)
+
+
+def test_patch_boundaries_c_entry_one_block_per_row():
+    # blt_patch_boundaries (no workspace, one block per row) against the oracle
+    L = _lib.lib()
+    for B, T in [(3, 1), (4, 8192), (2, 8193), (1, 20000)]:
+        H = np.abs(synth.normal_f32(60 + T, (B, T), 1.4, 0.6))
+        for mode, thr in ((0, 0.2), (1, 1.33)):
+            outs = [torch.empty((B, T), dtype=torch.int32, device=DEV) for _ in range(3)]
+            outs.append(torch.empty((B,), dtype=torch.int32, device=DEV))
+            Hd = cuda(H)
+            rc = L.blt_patch_boundaries(Hd.data_ptr(), B, T, ctypes.c_float(thr), mode,
+                                        *[t.data_ptr() for t in outs],
+                                        torch.cuda.current_stream().cuda_stream)
+            assert rc == 0, _lib.last_error()
+            _check_rule_outputs(H, thr, mode, outs)
+
+
 # ---------------------------------------------------------------- GEMM and attention
 @pytest.mark.parametrize("M,N,K", [(256, 256, 64), (1000, 320, 768), (4096, 2304, 768),
                                    (131072 // 8, 768, 2048)])
