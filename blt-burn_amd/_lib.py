@@ -46,6 +46,7 @@ EXPORTS = {
                                 c_vp]),
     "blt_patch_workspace_bytes": (c_i64, [c_i64, c_i64, c_i32]),
     "blt_patch_boundaries_rules": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_vp, c_vp, c_i64, c_vp]),
+    "blt_patch_boundaries_rules_noalloc": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_vp, c_vp]),
     "blt_entropy_patch_boundaries": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_vp, c_i32, c_vp, c_vp,
                                              c_i64, c_vp]),
     "blt_model_create": (c_i32, [c_i32, c_vp, c_vp, c_i64, ctypes.POINTER(c_vp)]),

@@ -335,6 +335,11 @@ int blt_patch_boundaries_rules(const float* H, int64_t B, int64_t T, int32_t n_r
   return launch_patch_rules(H, B, T, n_rules, rules, workspace, workspace_bytes, STREAM(stream));
 }
 
+int blt_patch_boundaries_rules_noalloc(const float* H, int64_t B, int64_t T, int32_t n_rules,
+                                       const blt_patch_rule* rules, blt_stream_t stream) {
+  return launch_patch_rules_noalloc(H, B, T, n_rules, rules, STREAM(stream));
+}
+
 int blt_entropy_patch_boundaries(const float* logits, int64_t B, int64_t T, int32_t vocab,
                                  float* entropies, int32_t n_rules, const blt_patch_rule* rules,
                                  void* workspace, int64_t workspace_bytes, blt_stream_t stream) {

@@ -33,6 +33,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 
 namespace blt {
 
@@ -473,6 +474,59 @@ int launch_entropy_patch(const float* logits, int64_t B, int64_t T, int vocab, f
   if (B == 0) return 0;
   if (T > 0 && !logits) return fail(BLT_ERR_INVALID, "entropy_patch: null logits");
   return launch_fused_variant(v, k, s);
+}
+
+// ---- the H pass with its workspace in a static device array ----------------
+// For callers that cannot allocate device memory (code under HIP graph
+// capture, tight serving loops): the per-tile counts and flag words live in
+// `scratch`, kScratchBytes on each device, instead of a caller workspace.
+// Nothing in it needs clearing (each call's flags kernel writes every word
+// the later kernels read), but every call on a device shares that device's
+// copy, so calls that overlap on one device race.
+constexpr int64_t kScratchBytes = 1 << 20;
+static __device__ __align__(256) uint64_t scratch[kScratchBytes / 8];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // scratch's device address, per device
+}  // namespace
+
+// The current device's copy of `scratch`, looked up with hipGetSymbolAddress
+// on the first call on that device (the array's host-side name is not a
+// device address).
+static int scratch_address(void** out) {
+  int dev = 0;
+  BLT_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return fail(BLT_ERR_NODEV, "patch scratch: device index");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    BLT_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(BLT_ERR_HIP, "patch scratch: no device address");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+int launch_patch_rules_noalloc(const float* H, int64_t B, int64_t T, int n_rules,
+                               const blt_patch_rule* rules, hipStream_t s) {
+  if (B < 0 || T < 0) return fail(BLT_ERR_SHAPE, "patch rules (no-alloc): negative shape");
+  if (n_rules < 1 || n_rules > 2)
+    return fail(BLT_ERR_INVALID, "patch rules (no-alloc): n_rules must be 1 or 2");
+  if (T > 0x7fffffff) return fail(BLT_ERR_SHAPE, "patch rules (no-alloc): T must fit int32");
+  if (8 * ws_words(B, T, n_rules, kTileH) > kScratchBytes)
+    return fail(BLT_ERR_SHAPE, "patch rules (no-alloc): n_rules * B * ceil(T / 1024) must be at "
+                               "most 7281 (1 MiB of static scratch)");
+  if (B == 0) {
+    PatchKArgs k{};
+    return fill_rules(k, n_rules, rules);
+  }
+  void* ws = nullptr;
+  int rc;
+  if ((rc = scratch_address(&ws))) return rc;
+  return launch_patch_rules(H, B, T, n_rules, rules, ws, kScratchBytes, s);
 }
 
 }  // namespace blt

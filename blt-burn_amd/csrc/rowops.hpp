@@ -53,6 +53,10 @@ int launch_patch_boundaries_varlen(const float* H, const int64_t* row_off, const
 int64_t patch_workspace_bytes(int64_t B, int64_t T, int n_rules);
 int launch_patch_rules(const float* H, int64_t B, int64_t T, int n_rules,
                        const blt_patch_rule* rules, void* ws, int64_t ws_bytes, hipStream_t s);
+// launch_patch_rules with the workspace in a static device array (1 MiB per
+// device; n_rules * B * ceil(T / 1024) <= 7281)
+int launch_patch_rules_noalloc(const float* H, int64_t B, int64_t T, int n_rules,
+                               const blt_patch_rule* rules, hipStream_t s);
 // softmax entropy of logits [B * T, vocab] (into H_out, may be NULL when the
 // vocab has a fused variant) and the rules in one pass
 int launch_entropy_patch(const float* logits, int64_t B, int64_t T, int vocab, float* H_out,

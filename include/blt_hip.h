@@ -166,6 +166,16 @@ int blt_patch_boundaries_rules(const float* H, int64_t B, int64_t T, int32_t n_r
                                const blt_patch_rule* rules, void* workspace,
                                int64_t workspace_bytes, blt_stream_t stream);
 
+/* blt_patch_boundaries_rules without the workspace argument: no counterpart in
+ * the reference.  For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops): the per-tile counts and flag words
+ * live in a static device array of 1 MiB per device, so it needs
+ * n_rules * B * ceil(T / 1024) <= 7281 (BLT_ERR_SHAPE otherwise) and calls no
+ * allocator.  Every call on one device shares that array: calls that overlap
+ * on one device race. */
+int blt_patch_boundaries_rules_noalloc(const float* H, int64_t B, int64_t T, int32_t n_rules,
+                                       const blt_patch_rule* rules, blt_stream_t stream);
+
 /* patcher::entropy (patcher.rs:15-22; NdArray form 38-63) followed by the
  * rules of blt_patch_boundaries_rules, in one pass over the logits when
  * vocab % 4 == 0, vocab < 1280 and the rows are 16-byte aligned (otherwise
