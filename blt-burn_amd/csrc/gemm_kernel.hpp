@@ -165,10 +165,12 @@ __device__ inline void epilogue(const GemmArgs& p, f32x16_t (&acc)[C::TM][C::TN]
           // past N (the last N tile of a 128-wide block can overhang by 64)
           if (col >= p.N) continue;
           float x1[4], x2[4];
+          // q heads of a QKV tile: the attention scale folded in before rounding
+          const float qs = col < p.q_cols ? p.q_scale : 1.f;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            x1[e] = acc[i][j][4 * g + e];
-            x2[e] = acc[i][j + 1][4 * g + e];
+            x1[e] = acc[i][j][4 * g + e] * qs;
+            x2[e] = acc[i][j + 1][4 * g + e] * qs;
           }
           if (p.epi == EPI_SILU_GATE) {
             const int64_t h = (col >> 6) * 32 + (col & 31);
@@ -545,11 +547,14 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int cl = j * 32 + 8 * g + 4 * lhalf;  // column within the wave tile
+          // q heads of a QKV tile: the attention scale rides on the row factor
+          const float rq = EPI == EPI_QKV_ROPE && col0 + j * 32 < p.q_cols ? rs[i] * p.q_scale
+                                                                           : rs[i];
           float x1[4], x2[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            x1[e] = acc[i][j][4 * g + e] * rs[i];
-            x2[e] = acc[i][j + 1][4 * g + e] * rs[i];
+            x1[e] = acc[i][j][4 * g + e] * rq;
+            x2[e] = acc[i][j + 1][4 * g + e] * rq;
           }
           if (silu) {
             // silu(g) * u with g = rs a1, u = rs a2 (rs > 0, the row factor):

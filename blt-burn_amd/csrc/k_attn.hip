@@ -11,12 +11,15 @@
 // (lane ^ 32) instead of a 32-lane reduction.  The output is accumulated
 // transposed, O^T = V^T . P^T, which keeps the per-query rescale factor in
 // the lane that owns the query.  The P^T registers feed the MFMA B operand
-// directly (no LDS round trip).  The softmax is VALU-bound (a v_exp_f32 per
-// score costs about three FMA issue slots), so the row sums of P come from
-// the MFMA pipe instead: a constant all-ones A operand times P^T gives every
-// lane its query's sum of the same bf16-rounded P the numerator uses.  V stays row-major in LDS; the V^T operand is
-// read with ds_read_b64_tr_b16, whose 16-lane transpose hands each lane 4
-// consecutive keys of one head-dim column.
+// directly (no LDS round trip).  The softmax is VALU-bound, so the rest of
+// the per-score work is kept off the VALU: q arrives scaled by log2(e) /
+// sqrt(64), and the first MFMA of each S^T chain starts from -m (the running
+// max) instead of zero, so S^T comes out of the matrix core ready for exp2;
+// the row sums of P are v_dot2_f32_bf16 over the same packed bf16 P the
+// numerator uses (16 per tile, a lane's half of the keys; the two halves
+// meet at the end).  V stays row-major in LDS; the V^T operand is read with
+// ds_read_b64_tr_b16, whose 16-lane transpose hands each lane 4 consecutive
+// keys of one head-dim column.
 //
 // Masking follows the reference's additive causal mask (model.rs:153-165:
 // key j visible to query i iff j <= i), extended with a window W > 0
@@ -116,6 +119,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
     for (int ks = 0; ks < 4; ++ks)
       qf[qq][ks] = __builtin_bit_cast(
           bf16x8_t, *reinterpret_cast<const u32x4_t*>(qrow + ks * 16 + lhalf * 8));
+    // q' = q log2(e) / sqrt(64) (unless the producer scaled it), rotated first
+    // when a RoPE table is given, rounded to bf16 once
+    const float qs = p.q_prescaled ? 1.f : kAttnQScale;
     if (p.q_rope_cs) {
       // fragments ks and ks + 2 hold the pair halves m and m + 32 of the same
       // 8 frequencies m = 16 ks + 8 lhalf + e: rotate them in registers
@@ -128,7 +134,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
         u32x4_t o1, o2;
 #pragma unroll
         for (int q2 = 0; q2 < 4; ++q2) {  // pairs 2 q2, 2 q2 + 1
-          const f32x4_t c = t[q2];        // (cos, sin) of pair 2 q2, then of pair 2 q2 + 1
+          const f32x4_t c = t[q2] * qs;   // (cos, sin) of pair 2 q2, then of pair 2 q2 + 1
           const float a0 = bf16_to_f32((uint16_t)(lo[q2] & 0xffff));
           const float a1 = bf16_to_f32((uint16_t)(lo[q2] >> 16));
           const float b0 = bf16_to_f32((uint16_t)(hi[q2] & 0xffff));
@@ -138,6 +144,16 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
         }
         qf[qq][ks] = __builtin_bit_cast(bf16x8_t, o1);
         qf[qq][ks + 2] = __builtin_bit_cast(bf16x8_t, o2);
+      }
+    } else if (!p.q_prescaled) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        u32x4_t w = __builtin_bit_cast(u32x4_t, qf[qq][ks]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[e] = pack_bf16x2(bf16_to_f32((uint16_t)(w[e] & 0xffff)) * qs,
+                             bf16_to_f32((uint16_t)(w[e] >> 16)) * qs);
+        qf[qq][ks] = __builtin_bit_cast(bf16x8_t, w);
       }
     }
   }
@@ -216,23 +232,25 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
   const int vt_lane = (4 * lhalf + (s16 >> 2)) * V_LD + 16 * ((lane >> 4) & 1) + 4 * (s16 & 3);
 
   f32x16_t o[NQ][2];
-  // lsum[qq][0]: running sum of P for this lane's query (every element of the
-  // accumulator holds it; only element 0 is rescaled and read)
-  f32x16_t lsum[NQ];
-  float m[NQ];
+  // m: the running max (log2 domain) of this lane's query, -inf until its
+  // first visible key; mu: the offset the scores are taken relative to (m, or
+  // 0 while m is -inf), held as -mu in every element of negm, the C operand
+  // of each S^T chain's first MFMA; l: this lane's half of the row sum of P
+  float m[NQ], mu[NQ], l[NQ];
+  f32x16_t negm[NQ];
 #pragma unroll
   for (int qq = 0; qq < NQ; ++qq) {
     m[qq] = -INFINITY;
+    mu[qq] = 0.f;
+    l[qq] = 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) lsum[qq][r] = 0.f;
+    for (int r = 0; r < 16; ++r) negm[qq][r] = 0.f;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[qq][j][r] = 0.f;
   }
-  const bf16x8_t ones = __builtin_bit_cast(
-      bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});  // bf16 1.0
-  const float sl2 = 0.125f * 1.44269504088896340736f;  // 1/sqrt(64) * log2(e)
+  const bf16x2_t ones2 = {(__bf16)1.0f, (__bf16)1.0f};
 
   issue(t_begin, 0);
   if (t_begin + 1 <= t_end) issue(t_begin + 1, 1);
@@ -251,13 +269,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
       const uint16_t* sv = sk + K_TILE;
       const int kb = t * BKV;
       // ---- S^T = K . Q^T (two 32-key sub-tiles x NQ query blocks) ----
+      // S^T - mu = K . Q'^T + negm: scores relative to the running max
       f32x16_t s[NQ][2];
-#pragma unroll
-      for (int qq = 0; qq < NQ; ++qq)
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) s[qq][sub][r] = 0.f;
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
@@ -266,12 +279,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
               *reinterpret_cast<const bf16x8_t*>(sk + kswz(sub * 32 + lrow, ks * 2 + lhalf));
 #pragma unroll
           for (int qq = 0; qq < NQ; ++qq)
-            s[qq][sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[qq][ks], s[qq][sub], 0, 0, 0);
+            s[qq][sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                a, qf[qq][ks], ks == 0 ? negm[qq] : s[qq][sub], 0, 0, 0);
         }
-      // ---- mask, online softmax (log2 domain, scale folded into one FMA) ----
-      // The running max used for exponentiation (m) only moves when a row's
-      // max grows by more than 2^8 (checked wave-wide), so P <= 256 and the
-      // O / l rescale is skipped for most tiles; O / l is unchanged by it.
+      // ---- mask, online softmax (log2 domain) ----
+      // The offset mu only moves when a row's max grows by more than 2^8 over
+      // it (checked wave-wide), so P <= 256 and the O / l rescale is skipped
+      // for most tiles; O / l is unchanged by it.
       // upper bound (causal diagonal, keys past T) and lower bound (window
       // edge, segment start) are applied only in the tiles that cross them
       const bool mask_hi = (p.causal && kb + BKV - 1 > qw) || (kb + BKV > T);
@@ -307,7 +321,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
               s[qq][sub][r] = ko > lo_rel ? s[qq][sub][r] : -INFINITY;
             }
         }
-        float mt = -INFINITY;
+        float mt = -INFINITY;  // this tile's max, relative to mu
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
@@ -317,19 +331,29 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
           // query: one VALU lane swap instead of an LDS permute round trip
           const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt),
                                                            __float_as_uint(mt), false, false);
-          mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * sl2;
+          mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
         }
-        if (__any(mt > m[qq] + 8.f)) {
-          const float m_new = fmaxf(m[qq], mt);
-          const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[qq] - m_new);
+        const bool grow = mt > 8.f || (m[qq] == -INFINITY && mt > -INFINITY);
+        if (__any(grow)) {
+          const float m_new = fmaxf(m[qq], mt + mu[qq]);  // m <= m_new
+          const float alpha = m[qq] == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[qq] - m_new);
           m[qq] = m_new;
-          lsum[qq][0] *= alpha;
+          const float mu_new = m_new == -INFINITY ? 0.f : m_new;
+          const float shift = mu_new - mu[qq];
+          mu[qq] = mu_new;
+          l[qq] *= alpha;
 #pragma unroll
           for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) o[qq][j][r] *= alpha;
+#pragma unroll
+          for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[qq][sub][r] -= shift;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) negm[qq][r] = -mu_new;
         }
-        const float m_use = m[qq] == -INFINITY ? 0.f : m[qq];
+        float ls = l[qq];
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
@@ -337,13 +361,15 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
             uint32_t w[4];
 #pragma unroll
             for (int e = 0; e < 8; e += 2) {
-              const float p0 = __builtin_amdgcn_exp2f(fmaf(s[qq][sub][8 * u + e], sl2, -m_use));
-              const float p1 =
-                  __builtin_amdgcn_exp2f(fmaf(s[qq][sub][8 * u + e + 1], sl2, -m_use));
+              const float p0 = __builtin_amdgcn_exp2f(s[qq][sub][8 * u + e]);
+              const float p1 = __builtin_amdgcn_exp2f(s[qq][sub][8 * u + e + 1]);
               w[e >> 1] = pack_bf16x2(p0, p1);
+              ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[e >> 1]), ones2,
+                                                    ls, false);
             }
             pb[qq][sub][u] = __builtin_bit_cast(bf16x8_t, u32x4_t{w[0], w[1], w[2], w[3]});
           }
+        l[qq] = ls;
       }
       // ---- O^T += V^T . P^T ----
 #pragma unroll
@@ -363,15 +389,6 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
               o[qq][dsub] =
                   __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[qq][sub][u], o[qq][dsub], 0, 0, 0);
           }
-      // ---- row sums: lsum += ones . P^T ----
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-          for (int qq = 0; qq < NQ; ++qq)
-            lsum[qq] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, pb[qq][sub][u], lsum[qq], 0,
-                                                               0, 0);
     }
     stage = stage + 1 < NSTAGE ? stage + 1 : 0;
   }
@@ -380,8 +397,11 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
 #pragma unroll
   for (int qq = 0; qq < NQ; ++qq) {
     const int qi = qw + 32 * qq + lrow;
+    // the query's row sum: this lane's keys plus its partner's (lane ^ 32)
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l[qq]),
+                                                     __float_as_uint(l[qq]), false, false);
+    const float lt = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
     if (qi >= T) continue;
-    const float lt = lsum[qq][0];
     // hardware reciprocal (1 ulp): the output is rounded to bf16
     const float inv = lt > 0.f ? __builtin_amdgcn_rcpf(lt) : 0.f;
     uint16_t* orow = p.o + b * p.sb_o + h * p.sh_o + (int64_t)qi * p.st_o;

@@ -278,6 +278,9 @@ int Model::forward(const int32_t* tokens, int64_t B, int64_t T, const blt_model_
     g.A = a; g.Bt = wqkv + l * 3 * D * D; g.C = qkv;
     g.M = M; g.N = 3 * D; g.K = D; g.lda = D; g.ldb = D; g.ldc = 3 * D;
     g.epi = EPI_QKV_ROPE; g.rope_cols = (int)(2 * D); g.seq_len = T; g.rope_cs = rope_cs;
+    // q leaves the GEMM scaled by log2(e) / sqrt(head_dim) (one bf16 rounding):
+    // the attention kernel's scores then come out of the MFMA in the log2 domain
+    g.q_cols = (int)D; g.q_scale = kAttnQScale;
     g.seg_start = seg_start;
     g.row_scale = rstd;
     if ((rc = launch_gemm(g, s))) return rc;
@@ -289,7 +292,7 @@ int Model::forward(const int32_t* tokens, int64_t B, int64_t T, const blt_model_
     at.sb_k = T * 3 * D; at.sh_k = 64; at.st_k = 3 * D;
     at.sb_v = T * 3 * D; at.sh_v = 64; at.st_v = 3 * D;
     at.sb_o = T * D; at.sh_o = 64; at.st_o = D;
-    at.causal = 1; at.window = cfg.window; at.seg_start = seg_start;
+    at.causal = 1; at.window = cfg.window; at.seg_start = seg_start; at.q_prescaled = 1;
     if ((rc = launch_attention(at, s))) return rc;
     if ((rc = mark(BLT_STAGE_ATTENTION, s))) return rc;
     g = GemmArgs{};

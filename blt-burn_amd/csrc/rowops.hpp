@@ -83,6 +83,8 @@ struct GemmArgs {
   int epi;
   int n_valid;      // EPI_F32
   int rope_cols;    // EPI_QKV_ROPE
+  int q_cols;       // EPI_QKV_ROPE: columns < q_cols (whole 64-column heads) are
+  float q_scale;    //   multiplied by q_scale before the bf16 rounding (0 = none)
   int64_t seq_len;  // EPI_QKV_ROPE: position = row % seq_len - seg_start[row]
   const int32_t* seg_start;  // segment starts within each row (NULL = 0)
   const float* rope_cs;  // [max_seqlen, 32, 2]
@@ -105,6 +107,9 @@ struct GemmArgs {
 int launch_gemm(const GemmArgs& a, hipStream_t s);
 
 // k_attn.hip -----------------------------------------------------------------
+// log2(e) / sqrt(64): the scores' scale in the log2 domain (q is multiplied by
+// it before its bf16 rounding, so S = q' k comes out of the MFMA ready for exp2)
+constexpr float kAttnQScale = 0.125f * 1.44269504088896340736f;
 struct AttnArgs {
   const uint16_t* q; const uint16_t* k; const uint16_t* v; uint16_t* o;
   int64_t B, H, T;
@@ -117,6 +122,9 @@ struct AttnArgs {
   // Optional: q is rotated (half-split RoPE pairs (m, m + 32)) as it is loaded,
   // with the (cos, sin) table [T, 32, 2] f32 at the query's row index.
   const float* q_rope_cs;
+  // q already multiplied by log2(e) / sqrt(64) (the QKV epilogue of the
+  // model); otherwise the kernel scales it as it is loaded
+  int q_prescaled;
 };
 int launch_attention(const AttnArgs& a, hipStream_t s);
 
