@@ -39,6 +39,8 @@ EXPORTS = {
     "blt_attention_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i32]),
     "blt_fused_attention_bf16": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i32]
                                  + [c_i64] * 9 + [c_i32, c_i32, c_f32, c_vp, c_vp]),
+    "blt_fused_attention_f32": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i32,
+                                        c_i32, c_vp]),
     "blt_rope_table_f32": (c_i32, [c_vp, c_i32, c_i32, c_f64, c_vp]),
     "blt_patch_boundaries": (c_i32, [c_vp, c_i64, c_i64, c_f32, c_i32, c_vp, c_vp, c_vp, c_vp,
                                      c_vp]),

@@ -280,6 +280,17 @@ int blt_fused_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_
   return launch_attention(a, s);
 }
 
+int blt_fused_attention_f32(const float* q, const float* k, const float* v, float* o, int64_t B,
+                            int64_t H, int64_t Tq, int64_t Tkv, int32_t d, int32_t causal,
+                            blt_stream_t stream) {
+  if (B < 0 || H < 0 || Tq < 0 || Tkv < 0) return fail(BLT_ERR_SHAPE, "attention_f32: negative shape");
+  if (d < 1 || d > 256) return fail(BLT_ERR_SHAPE, "attention_f32: head_dim must be 1 .. 256");
+  if (B == 0 || H == 0 || Tq == 0) return BLT_OK;
+  if (!q || !o || (Tkv > 0 && (!k || !v)))
+    return fail(BLT_ERR_INVALID, "attention_f32: null pointer");
+  return launch_attention_f32(q, k, v, o, B, H, Tq, Tkv, d, causal, STREAM(stream));
+}
+
 int blt_rope_table_f32(float* out_device, int32_t head_dim, int32_t max_seqlen, double theta,
                        blt_stream_t stream) {
   if (head_dim <= 0 || head_dim % 2 || max_seqlen < 0)

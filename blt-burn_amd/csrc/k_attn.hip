@@ -428,7 +428,129 @@ int run_attention(const AttnArgs& a, hipStream_t s) {
   return 0;
 }
 
+// ---- exact f32 attention: the reference kernel's semantics -----------------
+// fused_attention_kernel (attention_kernel.rs:20-125): any head_dim up to 256,
+// Tq and Tkv independent, causal means key j visible to query i iff j <= i,
+// scores (q . k) * (1 / sqrt(d)) and the softmax in f32 throughout.  One
+// block per (batch, head, 32 queries): the query tile, and 32-key tiles of K
+// and V, in LDS; thread t owns query t / 8 and, in the score step, keys
+// t % 8 + 8 m (m < 4), in the output step, head-dim columns t % 8 + 8 c; an
+// online softmax carries the running max and sum across key tiles.
+constexpr int FQ = 32, FK = 32, F_MAXD = 256;
+
+__global__ __launch_bounds__(256) void attn_f32_kernel(const float* __restrict__ q,
+                                                       const float* __restrict__ k,
+                                                       const float* __restrict__ v,
+                                                       float* __restrict__ o, int64_t H,
+                                                       int64_t Tq, int64_t Tkv, int d,
+                                                       int causal, float scale) {
+  extern __shared__ float smem[];
+  const int dp = d + 1;  // K row pitch: the 8 key rows a score step reads fall in distinct banks
+  float* Qs = smem;                // [FQ][d]
+  float* Ks = Qs + FQ * d;         // [FK][dp]
+  float* Vs = Ks + FK * dp;        // [FK][d]
+  float* Ps = Vs + FK * d;         // [FQ][FK + 1]
+  const int tid = threadIdx.x, qi = tid >> 3, g = tid & 7;
+  const int64_t q0 = (int64_t)blockIdx.x * FQ;
+  const int64_t bh = (int64_t)blockIdx.z * H + blockIdx.y;
+  const float* qb = q + bh * Tq * d;
+  const float* kb = k + bh * Tkv * d;
+  const float* vb = v + bh * Tkv * d;
+  for (int i = tid; i < FQ * d; i += 256) {
+    const int r = i / d;
+    Qs[i] = q0 + r < Tq ? qb[(q0 + r) * d + (i % d)] : 0.f;
+  }
+  const int nd = (d + 7) / 8;  // output columns per thread
+  float acc[F_MAXD / 8];
+#pragma unroll
+  for (int c = 0; c < F_MAXD / 8; ++c) acc[c] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  const int64_t qabs = q0 + qi;
+  const int64_t kend = causal ? (q0 + FQ < Tkv ? q0 + FQ : Tkv) : Tkv;
+  for (int64_t k0 = 0; k0 < kend; k0 += FK) {
+    __syncthreads();  // the previous tile's K, V and P are no longer read
+    for (int i = tid; i < FK * d; i += 256) {
+      const int r = i / d, e = i % d;
+      const bool in = k0 + r < Tkv;
+      Ks[r * dp + e] = in ? kb[(k0 + r) * d + e] : 0.f;
+      Vs[i] = in ? vb[(k0 + r) * d + e] : 0.f;
+    }
+    __syncthreads();
+    float sc[4];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int m2 = 0; m2 < 4; ++m2) {
+      const int kj = g + 8 * m2;
+      float dot = 0.f;
+      for (int e = 0; e < d; ++e) dot += Qs[qi * d + e] * Ks[kj * dp + e];
+      const int64_t kabs = k0 + kj;
+      const bool vis = kabs < Tkv && (!causal || kabs <= qabs);
+      sc[m2] = vis ? dot * scale : -INFINITY;
+      mt = fmaxf(mt, sc[m2]);
+    }
+    // the query's 32 scores of this tile sit in 8 consecutive lanes
+#pragma unroll
+    for (int x = 1; x < 8; x <<= 1) mt = fmaxf(mt, __shfl_xor(mt, x, 8));
+    const float m_new = fmaxf(m, mt);
+    const float alpha = m == -INFINITY ? (m_new == -INFINITY ? 1.f : 0.f) : expf(m - m_new);
+    float ls = 0.f;
+#pragma unroll
+    for (int m2 = 0; m2 < 4; ++m2) {
+      const float pv = m_new == -INFINITY ? 0.f : expf(sc[m2] - m_new);
+      Ps[qi * (FK + 1) + g + 8 * m2] = pv;
+      ls += pv;
+    }
+#pragma unroll
+    for (int x = 1; x < 8; x <<= 1) ls += __shfl_xor(ls, x, 8);
+    l = l * alpha + ls;
+    m = m_new;
+#pragma unroll
+    for (int c = 0; c < F_MAXD / 8; ++c) acc[c] *= alpha;
+    __syncthreads();  // P of the tile complete
+    for (int kj = 0; kj < FK; ++kj) {
+      const float pk = Ps[qi * (FK + 1) + kj];
+#pragma unroll
+      for (int c = 0; c < F_MAXD / 8; ++c) {
+        const int e = g + 8 * c;
+        if (c < nd && e < d) acc[c] += pk * Vs[kj * d + e];
+      }
+    }
+  }
+  if (qabs >= Tq) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  float* orow = o + (bh * Tq + qabs) * d;
+#pragma unroll
+  for (int c = 0; c < F_MAXD / 8; ++c) {
+    const int e = g + 8 * c;
+    if (c < nd && e < d) orow[e] = acc[c] * inv;
+  }
+}
+
 }  // namespace
+
+int launch_attention_f32(const float* q, const float* k, const float* v, float* o, int64_t B,
+                         int64_t H, int64_t Tq, int64_t Tkv, int d, int causal, hipStream_t s) {
+  if (B == 0 || H == 0 || Tq == 0) return 0;
+  if (d < 1 || d > F_MAXD) return fail(-2, "attention_f32: head_dim must be 1 .. 256");
+  if (H > 65535 || B > 65535 || (Tq + FQ - 1) / FQ > 0x7fffffff)
+    return fail(-2, "attention_f32: grid too large");
+  const size_t lds = (size_t)(FQ * d + FK * (d + 1) + FK * d + FQ * (FK + 1)) * sizeof(float);
+  if (lds > 64 * 1024) {
+    static bool raised = false;  // once: beyond the default 64 KB of dynamic LDS
+    if (!raised) {
+      BLT_HIP_CHECK(hipFuncSetAttribute((const void*)attn_f32_kernel,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)((FQ * F_MAXD + FK * (F_MAXD + 1) + FK * F_MAXD +
+                                               FQ * (FK + 1)) * sizeof(float))));
+      raised = true;
+    }
+  }
+  const dim3 grid((unsigned)((Tq + FQ - 1) / FQ), (unsigned)H, (unsigned)B);
+  hipLaunchKernelGGL(attn_f32_kernel, grid, dim3(256), lds, s, q, k, v, o, H, Tq, Tkv, d,
+                     causal ? 1 : 0, 1.0f / sqrtf((float)d));
+  BLT_LAUNCH_CHECK("attn_f32_kernel");
+  return 0;
+}
 
 int launch_attention(const AttnArgs& a, hipStream_t s) {
   if (a.B == 0 || a.H == 0 || a.T == 0) return 0;

@@ -127,5 +127,8 @@ struct AttnArgs {
   int q_prescaled;
 };
 int launch_attention(const AttnArgs& a, hipStream_t s);
+// f32 [B, H, Tq, d] x [B, H, Tkv, d] dense head-major, any d <= 256, f32 math
+int launch_attention_f32(const float* q, const float* k, const float* v, float* o, int64_t B,
+                         int64_t H, int64_t Tq, int64_t Tkv, int d, int causal, hipStream_t s);
 
 }  // namespace blt

@@ -128,15 +128,34 @@ def fused_coherence(norms, entropies, epsilon):
 
 
 def fused_attention(q, k, v, use_causal_mask, window=0, rope_theta=0.0):
-    """Scaled dot-product attention over [batch, heads, seq, head_dim] (mod.rs:225-236),
-    extended with a sliding window (0 = none) and RoPE (rope_theta > 0, half-split
-    pairs, model.rs:24-147).  head_dim must be 64.  QK^T and PV run on bf16 MFMA
-    with f32 softmax: f32 inputs are rounded to bf16 and the output is returned
-    in the input dtype."""
+    """Scaled dot-product attention over [batch, heads, seq, head_dim] (mod.rs:225-236).
+
+    f32 q, k, v without a window or RoPE: the reference kernel's semantics
+    (attention_kernel.rs:20-125) in f32 throughout, any head_dim <= 256, k and v
+    may have another seq length than q (causal: key j visible to query i iff
+    j <= i).  bf16 inputs (or a window > 0 / rope_theta > 0, this build's
+    extensions for the entropy model) take the MFMA path: head_dim 64, q, k, v
+    of one shape, QK^T and PV on bf16 MFMA with an f32 softmax; f32 inputs are
+    rounded to bf16 there and the output is returned in the input dtype."""
     require_cuda(q, k, v)
     _dtype_ok(q)
-    if q.dim() != 4 or q.shape != k.shape or q.shape != v.shape:
-        raise BltError("fused_attention expects q, k, v of one shape [batch, heads, seq, 64]")
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise BltError("fused_attention expects q, k, v [batch, heads, seq, head_dim]")
+    if (q.dtype == torch.float32 and k.dtype == torch.float32 and v.dtype == torch.float32 and
+            window == 0 and rope_theta == 0):
+        B, H, Tq, d = q.shape
+        if tuple(k.shape[:2]) != (B, H) or k.shape[3] != d or k.shape != v.shape:
+            raise BltError("fused_attention: k and v must be [batch, heads, seq_kv, head_dim] "
+                           "with q's batch, heads and head_dim")
+        qc, kc, vc = (contiguous(t) for t in (q, k, v))
+        o = torch.empty_like(qc)
+        check(_lib.lib().blt_fused_attention_f32(
+            qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(), B, H, Tq, kc.shape[2], d,
+            1 if use_causal_mask else 0, stream_ptr(qc.device)), "fused_attention")
+        return o
+    if q.shape != k.shape or q.shape != v.shape:
+        raise BltError("fused_attention (MFMA path) expects q, k, v of one shape "
+                       "[batch, heads, seq, 64]")
     B, H, T, d = q.shape
     in_dtype = q.dtype
     qb, kb, vb = (contiguous(t.to(torch.bfloat16)) for t in (q, k, v))

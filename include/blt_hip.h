@@ -120,6 +120,17 @@ int blt_fused_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_
                              int32_t causal, int32_t window, float rope_theta,
                              void* workspace, blt_stream_t stream);
 
+/* fused_attention on f32 tensors as the CubeCL kernel computes it
+ * (attention_kernel.rs:20-125, launched by backend.rs:334-383): q [B, H, Tq, d],
+ * k and v [B, H, Tkv, d], o [B, H, Tq, d], all f32, dense head-major; any
+ * head_dim d <= 256; causal: key j visible to query i iff j <= i.  Scores
+ * (q . k) / sqrt(d) and the softmax in f32 on the VALU (no bf16 rounding); a
+ * query that sees no key gets 0.  blt_fused_attention_bf16 is the MFMA path
+ * (d = 64, RoPE and windows) the model uses. */
+int blt_fused_attention_f32(const float* q, const float* k, const float* v, float* o, int64_t B,
+                            int64_t H, int64_t Tq, int64_t Tkv, int32_t d, int32_t causal,
+                            blt_stream_t stream);
+
 /* RoPE table, precompute_freqs_cis (model.rs:24-52): out [max_seqlen, head_dim/2, 2]
  * f32 (cos, sin), computed on the host in the reference's f32 order, copied to device. */
 int blt_rope_table_f32(float* out_device, int32_t head_dim, int32_t max_seqlen, double theta,

@@ -60,13 +60,15 @@ def lib():
                                          _f32p, _f32p]
         L.oracle_attention.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i32, _i32,
                                        _i32, ctypes.c_double]
+        L.oracle_attention_kernel.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64,
+                                              _i32, _i32]
         L.oracle_model_forward.argtypes = [ctypes.POINTER(Cfg), ctypes.POINTER(Weights), _i32p,
                                            _i64, _i64, _f32p, _f32p, _f32p, _f32p, _f32p]
         for f in ("oracle_entropy", "oracle_rms_norm", "oracle_l2_norm", "oracle_softmax",
                   "oracle_silu_gate", "oracle_coherence", "oracle_patch_mask",
                   "oracle_patch_indices", "oracle_patch_lengths", "oracle_patch_means",
                   "oracle_rope_table",
-                  "oracle_attention", "oracle_model_forward"):
+                  "oracle_attention", "oracle_attention_kernel", "oracle_model_forward"):
             getattr(L, f).restype = None
         _lib = L
     return _lib
@@ -202,6 +204,20 @@ def attention(q, k, v, causal=True, window=0, rope_theta=0.0):
     o = np.empty_like(q)
     lib().oracle_attention(pq, pk, pv, o.ctypes.data_as(_f32p), B, H, T, d, int(causal),
                            window, rope_theta)
+    return o
+
+
+def attention_kernel(q, k, v, causal=True):
+    """The reference's fused_attention_kernel: q f32 [B, H, Tq, d], k / v f32
+    [B, H, Tkv, d] -> o [B, H, Tq, d] (causal: key j visible to query i iff j <= i)."""
+    q, pq = _f(q)
+    k, pk = _f(k)
+    v, pv = _f(v)
+    B, H, Tq, d = q.shape
+    Tkv = k.shape[2]
+    o = np.empty_like(q)
+    lib().oracle_attention_kernel(pq, pk, pv, o.ctypes.data_as(_f32p), B, H, Tq, Tkv, d,
+                                  int(causal))
     return o
 
 

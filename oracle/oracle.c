@@ -23,6 +23,8 @@
  *   oracle_rope_table     fp64 closed form, identity at pos 0
  *   oracle_attention      fp64 numpy with a materialised mask; row 0 = v[0];
  *                         window >= T equals full causal
+ *   oracle_attention_kernel  fp64 numpy (any Tq, Tkv, d); one key -> v[0];
+ *                         equals oracle_attention when Tq = Tkv
  *   oracle_model_forward  fp64 numpy forward on tiny configs
  * The matmul/softmax summation order of burn-ndarray (matrixmultiply sgemm
  * blocking) is not reproduced; it moves results at the 1e-6 level only.
@@ -275,6 +277,52 @@ EXPORT void oracle_attention(const float* q, const float* k, const float* v, flo
     free(sc);
   }
   free(cs);
+}
+
+/* ---- fused_attention_kernel (attention_kernel.rs:20-125, launched by
+ * backend.rs:334-383): q [B, H, Tq, d], k / v [B, H, Tkv, d], one query at a
+ * time in three passes exactly as the kernel does them: the max of the visible
+ * scores, the sum of exp(score - max), then for each d the sum of
+ * exp(score - max) / sum * v.  score = (q . k) * (1 / sqrt(d)) in f32; with
+ * causal, key j is visible to query i iff j <= i (the same indices for any Tq
+ * and Tkv).  A query that sees no key gets 0. ---- */
+EXPORT void oracle_attention_kernel(const float* q, const float* k, const float* v, float* o,
+                                    int64_t B, int64_t H, int64_t Tq, int64_t Tkv, int32_t d,
+                                    int32_t causal) {
+  const float scale = 1.0f / sqrtf((float)d);
+#pragma omp parallel for schedule(dynamic)
+  for (int64_t bhq = 0; bhq < B * H * Tq; ++bhq) {
+    const int64_t bh = bhq / Tq, i = bhq % Tq;
+    const float* qr = q + (bh * Tq + i) * d;
+    const float* kb = k + bh * Tkv * d;
+    const float* vb = v + bh * Tkv * d;
+    float* orow = o + (bh * Tq + i) * d;
+    float mx = -INFINITY;
+    for (int64_t j = 0; j < Tkv; ++j) {
+      if (causal && j > i) continue;
+      float dot = 0.f;
+      for (int e = 0; e < d; ++e) dot += qr[e] * kb[j * d + e];
+      const float sc = dot * scale;
+      mx = sc > mx ? sc : mx;
+    }
+    float sum = 0.f;
+    for (int64_t j = 0; j < Tkv; ++j) {
+      if (causal && j > i) continue;
+      float dot = 0.f;
+      for (int e = 0; e < d; ++e) dot += qr[e] * kb[j * d + e];
+      sum += expf(dot * scale - mx);
+    }
+    for (int e = 0; e < d; ++e) {
+      float acc = 0.f;
+      for (int64_t j = 0; j < Tkv; ++j) {
+        if (causal && j > i) continue;
+        float dot = 0.f;
+        for (int e2 = 0; e2 < d; ++e2) dot += qr[e2] * kb[j * d + e2];
+        acc += expf(dot * scale - mx) / sum * vb[j * d + e];
+      }
+      orow[e] = acc;
+    }
+  }
 }
 
 /* ---- the entropy model ------------------------------------------------------ */

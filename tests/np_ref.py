@@ -74,6 +74,22 @@ def attention(q, k, v, causal=True, window=0, rope_theta=0.0):
     return softmax(s) @ v
 
 
+def attention_qkv(q, k, v, causal=True):
+    """[B, H, Tq, d] x [B, H, Tkv, d] float64 with a materialised mask (key j
+    visible to query i iff j <= i); a query that sees no key gets 0."""
+    q, k, v = (np.asarray(t, np.float64) for t in (q, k, v))
+    Tq, Tkv, d = q.shape[-2], k.shape[-2], q.shape[-1]
+    s = q @ np.swapaxes(k, -1, -2) / np.sqrt(d)
+    if causal:
+        vis = np.arange(Tkv)[None, :] <= np.arange(Tq)[:, None]
+        s = np.where(vis, s, -np.inf)
+    with np.errstate(invalid="ignore"):
+        mx = s.max(-1, keepdims=True)
+        e = np.exp(s - np.where(np.isfinite(mx), mx, 0.0))
+        w = e / np.maximum(e.sum(-1, keepdims=True), 1e-300)
+    return np.nan_to_num(w) @ v
+
+
 def model_forward(cfg, w, tokens):
     """cfg dict as oracle.model_forward; w: dict of float arrays in reference layouts."""
     D, L, Hn, F = cfg["dim"], cfg["n_layers"], cfg["n_heads"], cfg["hidden"]

@@ -404,6 +404,30 @@ def test_entropy_boundaries_graph_replay():
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("B,H,Tq,Tkv,d,causal", [(1, 2, 300, 300, 64, True),
+                                                 (2, 3, 70, 200, 32, True),
+                                                 (1, 2, 200, 70, 100, True),
+                                                 (1, 1, 97, 130, 256, False),
+                                                 (2, 2, 1, 33, 8, True),
+                                                 (1, 4, 129, 129, 128, False)])
+def test_attention_f32_reference_kernel(B, H, Tq, Tkv, d, causal):
+    # f32 fused_attention is the reference kernel's computation (any head_dim,
+    # seq_q != seq_kv) in f32: 1e-4 abs, far below one bf16 rounding of q, k, v
+    q = synth.normal_f32(80 + d, (B, H, Tq, d))
+    k = synth.normal_f32(81 + d, (B, H, Tkv, d))
+    v = synth.normal_f32(82 + d, (B, H, Tkv, d))
+    o = F.fused_attention(cuda(q), cuda(k), cuda(v), causal)
+    assert o.dtype == torch.float32 and tuple(o.shape) == (B, H, Tq, d)
+    np.testing.assert_allclose(o.cpu().numpy(), oracle.attention_kernel(q, k, v, causal),
+                               atol=1e-4, rtol=0)
+
+
+def test_attention_f32_rejects_wide_heads():
+    q = cuda(synth.normal_f32(90, (1, 1, 8, 264)))
+    with pytest.raises(_lib.BltError):
+        F.fused_attention(q, q, q, True)
+
+
 def test_attention_config3_b1():
     # config 3 shape at B=1 (the CPU comparison size): T=4096, 12 heads, window 512, RoPE
     o, ref = _attn_case(1, 12, 4096, True, 512, 10000.0, seed=synth.config_seed(3))

@@ -145,6 +145,31 @@ def test_attention_closed_forms():
     np.testing.assert_allclose(o1, v, atol=1e-6)
 
 
+@pytest.mark.parametrize("Tq,Tkv,d,causal", [(33, 33, 64, True), (20, 50, 16, True),
+                                              (50, 20, 100, True), (17, 40, 256, False),
+                                              (1, 7, 8, True)])
+def test_attention_kernel_vs_float64(Tq, Tkv, d, causal):
+    # the reference kernel's semantics: any head_dim, Tq != Tkv, causal j <= i
+    q = rng.normal(0, 1, (2, 3, Tq, d)).astype(np.float32)
+    k, v = (rng.normal(0, 1, (2, 3, Tkv, d)).astype(np.float32) for _ in range(2))
+    o = oracle.attention_kernel(q, k, v, causal)
+    np.testing.assert_allclose(o, np_ref.attention_qkv(q, k, v, causal), atol=2e-5)
+
+
+def test_attention_kernel_closed_forms():
+    q = rng.normal(0, 1, (1, 2, 30, 64)).astype(np.float32)
+    k, v = (rng.normal(0, 1, (1, 2, 30, 64)).astype(np.float32) for _ in range(2))
+    # the same semantics as the model's attention when Tq = Tkv
+    np.testing.assert_allclose(oracle.attention_kernel(q, k, v, True),
+                               oracle.attention(q, k, v, True, 0, 0.0), atol=1e-5)
+    # one key: every query returns it
+    o1 = oracle.attention_kernel(q, k[:, :, :1], v[:, :, :1], False)
+    np.testing.assert_allclose(o1, np.broadcast_to(v[:, :, :1], o1.shape), atol=1e-6)
+    # causal row 0 sees only key 0
+    np.testing.assert_allclose(oracle.attention_kernel(q, k, v, True)[:, :, 0], v[:, :, 0],
+                               atol=1e-6)
+
+
 def _tiny_model(hidden=128, L=2, D=128, H=2, V=260, seed=5):
     r = np.random.default_rng(seed)
     g = lambda *s: r.normal(0, 0.05, s).astype(np.float32)  # noqa: E731
