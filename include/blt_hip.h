@@ -337,8 +337,11 @@ int blt_tokenize_documents(const uint8_t* bytes, const int64_t* byte_offsets, in
  * documents at once.  Chunks of at most chunk_len tokens (the first covers
  * [0, chunk_len - overlap); later ones start overlap tokens early and drop
  * their first overlap outputs) are packed into batches of `rows` rows of
- * `row_len` tokens, each chunk its own attention / RoPE segment; a document
- * always lies in one batch. */
+ * `row_len` tokens, each chunk its own attention / RoPE segment.  A document
+ * whose chunks fit one batch lies in one batch; a longer one (any length) is
+ * cut into groups of consecutive chunks that each fit a batch, and its boundary
+ * pass runs once its last group has landed.  Host packing of batch i + 1
+ * overlaps the device work of batch i. */
 typedef struct blt_ingest_config {
   int32_t rows;            /* packed rows per batch */
   int32_t row_len;         /* tokens per packed row (<= model max_seqlen) */
