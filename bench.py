@@ -60,7 +60,8 @@ def _dispatch_stages(names, layers):
             out.append("rmsnorm")
         elif "entropy_" in n and "_kernel" in n:
             out.append("entropy")
-        elif "patch_boundary_kernel" in n or "patch_tile_kernel" in n:
+        elif ("patch_boundary_kernel" in n or "patch_flags_kernel" in n or
+              "patch_scan_kernel" in n or "patch_compact_kernel" in n):
             out.append("patch_boundaries")
         elif "embed_kernel" in n:
             out.append("embed")
