@@ -207,20 +207,28 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs p) {
     const int64_t k0 = (int64_t)t * BKV;
     const char* kb0 = reinterpret_cast<const char*>(kbase + k0 * p.st_k);
     const char* vb0 = reinterpret_cast<const char*>(vbase + k0 * p.st_v);
-    const bool full = k0 + BKV <= T;  // uniform
     const unsigned sb = lds_base + (unsigned)(stage * STAGE * 2);
-#pragma unroll
-    for (int q = 0; q < QMAX; ++q) {
-      if (q == QMAX - 1 && nops < QMAX) break;
+    auto op = [&](int q, uint32_t off) {
       const int o = wid_u + 4 * q;
-      const bool isk = q < 2;
-      uint32_t off = goff[q];
-      if (!full) {
-        const int64_t back = k0 + gkey[q] < T ? 0 : k0 + gkey[q] - (T - 1);  // rows to step back
-        off -= (uint32_t)(back * (isk ? p.st_k : p.st_v) * 2);
+      const unsigned la = q < 2 ? sb + (unsigned)(o * 1024)
+                                : sb + (unsigned)(K_TILE * 2 + (o - NKOP) * 1024);
+      dma16_so(q < 2 ? kb0 : vb0, off, la);
+    };
+    // a whole tile (uniform, 32-bit: T < 2^30) takes the precomputed offsets
+    // as they are; only the row's last, partial tile steps rows back
+    if (t * BKV + BKV <= T) {
+#pragma unroll
+      for (int q = 0; q < QMAX; ++q) {
+        if (q == QMAX - 1 && nops < QMAX) break;
+        op(q, goff[q]);
       }
-      const unsigned la = isk ? sb + (unsigned)(o * 1024) : sb + (unsigned)(K_TILE * 2 + (o - NKOP) * 1024);
-      dma16_so(isk ? kb0 : vb0, off, la);
+    } else {
+#pragma unroll
+      for (int q = 0; q < QMAX; ++q) {
+        if (q == QMAX - 1 && nops < QMAX) break;
+        const int64_t back = k0 + gkey[q] < T ? 0 : k0 + gkey[q] - (T - 1);  // rows to step back
+        op(q, goff[q] - (uint32_t)(back * (q < 2 ? p.st_k : p.st_v) * 2));
+      }
     }
   };
 
