@@ -543,16 +543,11 @@ int launch_attention_f32(const float* q, const float* k, const float* v, float* 
   if (H > 65535 || B > 65535 || (Tq + FQ - 1) / FQ > 0x7fffffff)
     return fail(-2, "attention_f32: grid too large");
   const size_t lds = (size_t)(FQ * d + FK * (d + 1) + FK * d + FQ * (FK + 1)) * sizeof(float);
-  if (lds > 64 * 1024) {
-    static bool raised = false;  // once: beyond the default 64 KB of dynamic LDS
-    if (!raised) {
-      BLT_HIP_CHECK(hipFuncSetAttribute((const void*)attn_f32_kernel,
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        (int)((FQ * F_MAXD + FK * (F_MAXD + 1) + FK * F_MAXD +
-                                               FQ * (FK + 1)) * sizeof(float))));
-      raised = true;
-    }
-  }
+  // beyond the default 64 KB of dynamic LDS the kernel's limit is raised (a
+  // host-side setting of the current device, set on every such launch)
+  if (lds > 64 * 1024)
+    BLT_HIP_CHECK(hipFuncSetAttribute((const void*)attn_f32_kernel,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
   const dim3 grid((unsigned)((Tq + FQ - 1) / FQ), (unsigned)H, (unsigned)B);
   hipLaunchKernelGGL(attn_f32_kernel, grid, dim3(256), lds, s, q, k, v, o, H, Tq, Tkv, d,
                      causal ? 1 : 0, 1.0f / sqrtf((float)d));
