@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdint.h>
 #include <string>
 
@@ -127,6 +128,59 @@ __device__ inline int wave_incl_scan(int v) {
   v += dpp_i32<0x143, 0xC>(v);
   return v;
 }
+// max / sum over each 32-lane half of the wave, in every lane of the half
+__device__ inline float half_max(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  float a, b;
+  swap_pair<16>(v, a, b);
+  return fmaxf(a, b);
+}
+__device__ inline float half_sum(float v) {
+  v = sum16(v);
+  float a, b;
+  swap_pair<16>(v, a, b);
+  return a + b;
+}
+
+// Softmax entropy (natural log) of one row held by the 32 lanes of a half
+// wave: lane l has elements c * 128 + 4 l .. + 3 in v[c] (c < NH) and
+// NH * 128 + 32 q + l in t[q] (-inf past the row's end).  With d = x - max
+// and p = e^d, H = log sum p - sum(p d) / sum p, the same quantity as
+// -sum exp(lsm) lsm; padding (-inf) contributes 0.  Shared by every kernel
+// that computes entropies of rows below 512 elements, so their values agree
+// bit for bit.
+template <int NH, int VT>
+__device__ inline float entropy_half_row(const float (&v)[NH > 0 ? NH : 1][4],
+                                         const float (&t)[VT > 0 ? VT : 1]) {
+  float m = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < NH; ++c)
+    m = fmaxf(m, fmaxf(fmaxf(v[c][0], v[c][1]), fmaxf(v[c][2], v[c][3])));
+#pragma unroll
+  for (int q = 0; q < VT; ++q) m = fmaxf(m, t[q]);
+  m = half_max(m);
+  float sp = 0.f, sd = 0.f;
+  auto acc = [&](float xv) {
+    const float d = fmaxf(xv - m, -1e30f);
+    const float pe = __expf(d);
+    sp += pe;
+    sd = fmaf(pe, d, sd);
+  };
+#pragma unroll
+  for (int c = 0; c < NH; ++c)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc(v[c][k]);
+#pragma unroll
+  for (int q = 0; q < VT; ++q) acc(t[q]);
+  sp = half_sum(sp);
+  sd = half_sum(sd);
+  // hardware reciprocal (1 ulp) for the one quotient per row
+  return __logf(sp) - sd * __builtin_amdgcn_rcpf(sp);
+}
+
 __device__ inline float wave_max(float v) {
   v = fmaxf(v, dpp_f32<0xB1>(v));
   v = fmaxf(v, dpp_f32<0x4E>(v));

@@ -239,6 +239,60 @@ __global__ __launch_bounds__(W * 64) void entropy_flags_kernel(PatchKArgs a) {
   if (wid < a.n_rules) tile_flags<1>(a, wid, b, t0, tile, hs, lane);
 }
 
+// The same pass for rows below 512 elements: 32 lanes per row
+// (entropy_half_row, the arithmetic of the entropy kernel for such rows), so
+// wave w takes positions t0 + 4 w .. + 3 as two pairs, and wave 0 also t0 - 1
+// (its upper half computes a copy).  All of a wave's rows are loaded first.
+template <int NH, int VT, int W>
+__global__ __launch_bounds__(W * 64) void entropy_flags_half_kernel(PatchKArgs a) {
+  constexpr int R = kTileL / W;  // rows per wave
+  static_assert(R % 2 == 0, "rows go in pairs");
+  constexpr int P = R / 2;
+  __shared__ float hs[kTileL + 4];
+  const uint32_t tile = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, l32 = lane & 31, hf = lane >> 5;
+  const int64_t T = a.T;
+  const int64_t b = tile / (uint32_t)a.tpr;
+  const int64_t t0 = (int64_t)(tile % (uint32_t)a.tpr) * kTileL;
+  const int64_t rowoff = b * T, p0 = t0 + wid * R;
+  const int n = a.vocab;
+  auto load = [&](int64_t p, float (&v)[NH > 0 ? NH : 1][4], float (&t)[VT > 0 ? VT : 1]) {
+    p = p < 0 ? 0 : (p >= T ? T - 1 : p);
+    const float* xr = a.logits + (rowoff + p) * (int64_t)n;
+#pragma unroll
+    for (int c = 0; c < NH; ++c) {
+      const float4 q = *reinterpret_cast<const float4*>(xr + c * 128 + l32 * 4);
+      v[c][0] = q.x; v[c][1] = q.y; v[c][2] = q.z; v[c][3] = q.w;
+    }
+#pragma unroll
+    for (int q = 0; q < VT; ++q) {
+      const int e = NH * 128 + q * 32 + l32;
+      t[q] = e < n ? xr[e] : -INFINITY;
+    }
+  };
+  if (T > 0) {
+    float v[P][NH > 0 ? NH : 1][4], t[P][VT > 0 ? VT : 1];
+    float vl[NH > 0 ? NH : 1][4], tl[VT > 0 ? VT : 1];
+#pragma unroll
+    for (int j = 0; j < P; ++j) load(p0 + 2 * j + hf, v[j], t[j]);
+    const bool left = wid == 0 && t0 > 0;  // uniform
+    if (left) load(t0 - 1, vl, tl);
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      const float H = entropy_half_row<NH, VT>(v[j], t[j]);
+      const int64_t p = p0 + 2 * j + hf;
+      if (l32 == 0 && p < T) hs[1 + wid * R + 2 * j + hf] = H;
+    }
+    if (left) {
+      const float H = entropy_half_row<NH, VT>(vl, tl);
+      if (lane == 0) hs[0] = H;
+    }
+  }
+  __syncthreads();
+  if (wid == W - 1 && a.H_out && t0 + lane < T) a.H_out[rowoff + t0 + lane] = hs[1 + lane];
+  if (wid < a.n_rules) tile_flags<1>(a, wid, b, t0, tile, hs, lane);
+}
+
 // ---- exclusive prefixes of long rows: one wave per (row, rule) ---------------
 __global__ __launch_bounds__(64) void patch_scan_kernel(PatchKArgs a) {
   const int64_t b = blockIdx.x / a.n_rules;
@@ -409,14 +463,31 @@ int launch_fused(const PatchKArgs& k, hipStream_t s) {
   return launch_tail(k, s);
 }
 
-// (NF, VT) of the register layout of entropy_tail_kernel; -1 when the row
-// width has none (the caller then runs entropy and the H pass apart)
+template <int NH, int VT>
+int launch_fused_half(const PatchKArgs& k, hipStream_t s) {
+  hipLaunchKernelGGL((entropy_flags_half_kernel<NH, VT, kFusedWaves>), dim3(k.ntiles),
+                     dim3(kFusedWaves * 64), 0, s, k);
+  BLT_LAUNCH_CHECK("entropy_flags_half_kernel");
+  return launch_tail(k, s);
+}
+
+// The register layout of the entropy kernel for this row width: below 512
+// elements the half-wave rows (NH, VT) of entropy_half_kernel (variants
+// 100 + NH * 8 + VT), else (NF, VT) of entropy_tail_kernel; -1 when the width
+// has none (the caller then runs entropy and the H pass apart)
 int fused_variant(int n) {
   if (n <= 0 || n % 4 || n >= 1280) return -1;
+  if (n < 512) return 100 + (n / 128) * 8 + (n % 128 + 31) / 32;
   return (n / 256) * 8 + (n % 256 + 63) / 64;
 }
 int launch_fused_variant(int v, const PatchKArgs& k, hipStream_t s) {
   switch (v) {
+#define BLT_FH(NH, VT) case 100 + NH * 8 + VT: return launch_fused_half<NH, VT>(k, s);
+    BLT_FH(0, 1) BLT_FH(0, 2) BLT_FH(0, 3) BLT_FH(0, 4)
+    BLT_FH(1, 0) BLT_FH(1, 1) BLT_FH(1, 2) BLT_FH(1, 3) BLT_FH(1, 4)
+    BLT_FH(2, 0) BLT_FH(2, 1) BLT_FH(2, 2) BLT_FH(2, 3) BLT_FH(2, 4)
+    BLT_FH(3, 0) BLT_FH(3, 1) BLT_FH(3, 2) BLT_FH(3, 3) BLT_FH(3, 4)
+#undef BLT_FH
 #define BLT_FV(NF, VT) case NF * 8 + VT: return launch_fused<NF, VT>(k, s);
     BLT_FV(0, 1) BLT_FV(0, 2) BLT_FV(0, 3) BLT_FV(0, 4)
     BLT_FV(1, 0) BLT_FV(1, 1) BLT_FV(1, 2) BLT_FV(1, 3) BLT_FV(1, 4)

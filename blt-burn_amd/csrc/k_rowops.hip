@@ -104,6 +104,32 @@ __global__ __launch_bounds__(256) void entropy_kernel(const T* __restrict__ logi
   if (lane == 0) out[row] = -h;
 }
 
+// Rows below 512 elements (n % 4 == 0, aligned): 32 lanes per row, two rows
+// per wave, eight per block.  A row of 260 f32 logits is two 16-byte loads
+// and one element per lane instead of one load and a 4-element tail over 64
+// lanes, so a wave's reductions and exponentials serve two rows at once
+// (config 1: 5.5 us for 32,768 rows against 7.6 us one row per wave).  The
+// upper half of a wave past the last row computes a valid row and stores
+// nothing (both halves run the cross-lane steps).
+template <typename T, int NH, int VT>
+__global__ __launch_bounds__(256) void entropy_half_kernel(const T* __restrict__ logits,
+                                                           float* __restrict__ out,
+                                                           int64_t rows, int n) {
+  const int l32 = threadIdx.x & 31;
+  const int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  const T* x = logits + (row < rows ? row : rows - 1) * n;
+  float v[NH > 0 ? NH : 1][4], t[VT > 0 ? VT : 1];
+#pragma unroll
+  for (int c = 0; c < NH; ++c) ld4(x, c * 128 + l32 * 4, v[c]);
+#pragma unroll
+  for (int q = 0; q < VT; ++q) {
+    const int e = NH * 128 + q * 32 + l32;
+    t[q] = e < n ? ld1(x, e) : -INFINITY;
+  }
+  const float H = entropy_half_row<NH, VT>(v, t);
+  if (l32 == 0 && row < rows) out[row] = H;
+}
+
 // Rows of n = 256 NF + 64 (VT - 1) + r elements (n % 4 == 0, NF <= 4, VT <= 4):
 // NF full chunks of 256 (16-byte loads, 4 per lane) and a tail of VT
 // elements per lane (e = 256 NF + 64 q + lane), so no lane computes an
@@ -769,8 +795,35 @@ struct EntropyL {
     }
     return -1;
   }
+  template <int NH, int VT>
+  static int half(const Args& a) {
+    hipLaunchKernelGGL((entropy_half_kernel<T, NH, VT>), dim3(ceil_div(a.rows, 8)), dim3(256), 0,
+                       a.s, a.x, a.out, a.rows, a.n);
+    BLT_LAUNCH_CHECK("entropy_half_kernel");
+    return 0;
+  }
+  template <int NH>
+  static int half_vt(const Args& a, int vt) {
+    switch (vt) {
+      case 0: return NH > 0 ? half<NH, 0>(a) : -1;
+      case 1: return half<NH, 1>(a);
+      case 2: return half<NH, 2>(a);
+      case 3: return half<NH, 3>(a);
+      case 4: return half<NH, 4>(a);
+    }
+    return -1;
+  }
   // n % 4 == 0 with 16-byte (f32) / 8-byte (bf16) aligned rows, n < 1280
   static int fast(const Args& a) {
+    if (a.n < 512) {
+      const int vt = (a.n % 128 + 31) / 32;
+      switch (a.n / 128) {
+        case 0: return half_vt<0>(a, vt);
+        case 1: return half_vt<1>(a, vt);
+        case 2: return half_vt<2>(a, vt);
+        case 3: return half_vt<3>(a, vt);
+      }
+    }
     const int nf = a.n / 256, vt = (a.n % 256 + 63) / 64;
     switch (nf) {
       case 0: return tail_vt<0>(a, vt);

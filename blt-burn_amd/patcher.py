@@ -129,6 +129,45 @@ def entropy_patch_boundaries(logits, rules, out=None, entropies=None):
     return entropies, outs
 
 
+class EntropyPatchPlan:
+    """entropy_patch_boundaries prepared for repeated calls on logits of one
+    shape, as a serving loop makes them: the entropies and rule outputs are
+    allocated, the rule array and the workspace bound, once; each call checks
+    the logits and makes the one library call (the per-call checks of a dozen
+    tensors cost the function form more host time than the device pass).
+    Calls return the same output tensors each time and must be stream-ordered
+    with any other boundary pass that shares the device's workspace."""
+
+    def __init__(self, batch, seq, vocab, rules, device=None):
+        dev = torch.device("cuda" if device is None else device)
+        if dev.index is None:
+            dev = torch.device("cuda", torch.cuda.current_device())
+        rules = list(rules)
+        self.shape = (int(batch), int(seq), int(vocab))
+        self.device = dev
+        self.entropies = torch.empty((batch, seq), dtype=torch.float32, device=dev)
+        self.outs = [_rule_outputs(batch, seq, dev, None) for _ in rules]
+        self._arr = _rules_struct(rules, self.outs)
+        L = _lib.lib()
+        self._ws = _workspace(dev, L.blt_patch_workspace_bytes(batch, seq, len(rules)))
+        self._fn = L.blt_entropy_patch_boundaries
+        self._tail = (self.entropies.data_ptr(), len(rules), self._arr, self._ws.data_ptr(),
+                      self._ws.numel())
+
+    def __call__(self, logits):
+        """logits: f32 [batch, seq, vocab] on the plan's device, contiguous.
+        Returns (entropies, [(mask, starts, lengths, counts) per rule])."""
+        if not (isinstance(logits, torch.Tensor) and logits.dtype == torch.float32 and
+                logits.shape == self.shape and logits.device == self.device and
+                logits.is_contiguous()):
+            raise BltError("EntropyPatchPlan expects contiguous f32 logits %s on %s"
+                           % (list(self.shape), self.device))
+        B, T, V = self.shape
+        check(self._fn(logits.data_ptr(), B, T, V, *self._tail, stream_ptr(self.device)),
+              "entropy_patch_boundaries")
+        return self.entropies, self.outs
+
+
 def patch_boundaries(entropies, threshold, mode=PATCH_MONOTONIC, out=None):
     """Device pass over entropies [batch, seq] f32.  Returns (mask, starts, lengths,
     counts): mask [B, T] int32, starts/lengths [B, T] int32 with counts[b] valid

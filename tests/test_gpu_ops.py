@@ -291,6 +291,31 @@ def test_patch_rules_workspace_reused_across_sizes():
             _check_rule_outputs(Hd.cpu().numpy(), thr, mode, o)
 
 
+def test_entropy_patch_plan_matches_function():
+    # the prepared call returns what the function returns, call after call, and
+    # rejects logits of another shape, dtype or layout
+    B, T, V = 3, 1000, 260
+    rules = [(patcher.PATCH_GLOBAL, 1.33), (patcher.PATCH_MONOTONIC, 0.2)]
+    plan = patcher.EntropyPatchPlan(B, T, V, rules)
+    for k in range(3):
+        x = cuda(synth.normal_f32(400 + k, (B, T, V), 0.0, 2.0))
+        Hp, outs_p = plan(x)
+        Hf, outs_f = patcher.entropy_patch_boundaries(x, rules)
+        assert torch.equal(Hp, Hf)
+        for op, of in zip(outs_p, outs_f):
+            for a, b in zip(op, of):
+                if a.dim() == 2:  # starts / lengths: the valid entries of each row
+                    for r in range(B):
+                        n = int(of[3][r])
+                        assert torch.equal(a[r, :n], b[r, :n])
+                else:
+                    assert torch.equal(a, b)
+        _check_rule_outputs(Hf.cpu().numpy(), 0.2, patcher.PATCH_MONOTONIC, outs_p[1])
+    for bad in (x[:, :500], x.to(torch.float64), x.transpose(0, 1), x.cpu()):
+        with pytest.raises(_lib.BltError):
+            plan(bad)
+
+
 def test_patch_boundaries_c_entry_one_block_per_row():
     # blt_patch_boundaries (no workspace, one block per row) against the oracle
     L = _lib.lib()
