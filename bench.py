@@ -439,6 +439,9 @@ def bench_config1(args):
     ms = _timed(step, steps, args.warmup)
     ms_fn = _timed(step_fn, steps, args.warmup)
     ms_k = _graph_launch_ms(step, 20)
+    # the entropy kernel alone on the same logits (fused_entropy), for its HBM rate
+    from blt_burn_amd import fused_ops
+    ms_e = _graph_launch_ms(lambda: fused_ops.fused_entropy(logits, V), 20)
     n = B * T
     counts = [int(bnd[r][3].sum()) for r in range(2)]
     # logits read, entropies written, both masks, the starts and lengths written
@@ -464,6 +467,11 @@ def bench_config1(args):
                                       "traffic": None, "launch_ms": round(ms_k, 5),
                                       "bytes_per_launch": k_bytes}),
         "starts": {"global": counts[0], "monotonic": counts[1]},
+        "entropy_kernel_only": {"kernel": "entropy_half_kernel<float, 2, 1> (fused_entropy)",
+                                "ms": round(ms_e, 5),
+                                "GB/s": round(n * (V * 4 + 4) / (ms_e * 1e-3) / 1e9, 1),
+                                "frac": round(n * (V * 4 + 4) / (ms_e * 1e-3) / 1e9 /
+                                              PEAK_HBM_GBS, 4)},
         "cpu_baseline": None,
     }
     if not args.no_cpu:
