@@ -13,6 +13,6 @@ __version__ = "0.1.0"
 def __getattr__(name):
     # torch-dependent submodules load lazily so synth/_lib work without torch
     import importlib
-    if name in ("fused_ops", "patcher", "model", "ingest"):
+    if name in ("fused_ops", "patcher", "model", "ingest", "pipeline"):
         return importlib.import_module("." + name, __name__)
     raise AttributeError(name)

@@ -64,6 +64,13 @@ EXPORTS = {
     "blt_ingest_last_stats": (c_i32, [c_vp, c_vp]),
     "blt_ingest_run": (c_i32, [c_vp, c_vp, c_vp, c_i64] + [c_vp] * 7),
     "blt_ingest_run_patch_means": (c_i32, [c_vp, c_vp, c_vp, c_i64] + [c_vp] * 10),
+    "blt_pipeline_create": (c_i32, [c_vp, c_f64, c_vp]),
+    "blt_pipeline_destroy": (c_i32, [c_vp]),
+    "blt_pipeline_process_chunk": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_i64] + [c_vp] * 6),
+    "blt_pipeline_accumulated": (c_i32, [c_vp, c_vp]),
+    "blt_pipeline_read": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp]),
+    "blt_pipeline_process_documents": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_vp,
+                                               c_i64] + [c_vp] * 6),
     "blt_model_set_profiling": (c_i32, [c_vp, c_i32]),
     "blt_model_read_profile": (c_i32, [c_vp, ctypes.POINTER(c_f64), ctypes.POINTER(c_i64), c_i32]),
     "blt_stage_name": (ctypes.c_char_p, [c_i32]),

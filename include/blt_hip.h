@@ -394,6 +394,65 @@ typedef struct blt_ingest_stats {
 } blt_ingest_stats;
 int blt_ingest_last_stats(blt_ingest* g, blt_ingest_stats* out);
 
+/* Streaming pipeline (pipeline.rs) ------------------------------------------ */
+
+/* pipeline.rs:37-43: chunks of BLT_PIPELINE_CHUNK_SIZE raw bytes, every later
+ * chunk starting BLT_PIPELINE_STRIDE bytes early; patches that start before
+ * chunk start + BLT_PIPELINE_SAFE_ZONE_END are confirmed. */
+#define BLT_PIPELINE_CHUNK_SIZE 4096
+#define BLT_PIPELINE_STRIDE 2048
+#define BLT_PIPELINE_SAFE_ZONE_END 2048
+
+/* PipelineBuffer (pipeline.rs:74-104) bound to one model: the accumulated
+ * entropies and norms stay in device memory, the raw bytes in host memory.
+ * threshold is the monotonic rule's delta (patcher.rs:80-118, compared in
+ * f32 as the reference's greater_elem does). */
+typedef struct blt_pipeline blt_pipeline;
+int blt_pipeline_create(blt_model* m, double threshold, blt_pipeline** out);
+int blt_pipeline_destroy(blt_pipeline* p);
+
+/* PipelineBuffer::process_chunk (pipeline.rs:111-238): one forward of the raw
+ * bytes (tokens = byte values, no +4 offset, pipeline.rs:123) as a [1, n]
+ * batch, the new outputs appended (all of the first chunk, the part after
+ * BLT_PIPELINE_STRIDE of later ones), the monotonic boundary pass over what
+ * has accumulated, and the patches it confirms: patch i starts at start[i],
+ * spans length[i] bytes (to the next start, or to the end of what has
+ * accumulated) and has the left-to-right f32 means of the norms (prominence)
+ * and entropies over that span (pipeline.rs:240-258).  *n_patches receives
+ * the count; at most min(cutoff, accumulated) - lower are written, where
+ * lower / cutoff are the reference's confirmation window, so cap >= the
+ * accumulated length after the call always suffices (BLT_ERR_SHAPE before
+ * any work otherwise).  The work runs on `stream` (ordered after the caller's
+ * earlier work there); returns when every output is written. */
+int blt_pipeline_process_chunk(blt_pipeline* p, const uint8_t* chunk, int64_t n, int32_t is_last,
+                               int64_t cap, int64_t* start, int64_t* length, float* prominence,
+                               float* entropy, int64_t* n_patches, blt_stream_t stream);
+/* Number of accumulated positions (PipelineBuffer::entropies().len()). */
+int blt_pipeline_accumulated(blt_pipeline* p, int64_t* len);
+/* PipelineBuffer::entropies / norms / raw_bytes (pipeline.rs:260-273): copies
+ * positions [offset, offset + n) of each non-null output. */
+int blt_pipeline_read(blt_pipeline* p, int64_t offset, int64_t n, float* entropies, float* norms,
+                      uint8_t* raw_bytes, blt_stream_t stream);
+
+/* process_document (pipeline.rs:279-324) for n_docs documents at once:
+ * document d is bytes[doc_offsets[d], doc_offsets[d + 1]).  The chunks of
+ * every document run as independent segments of packed [rows, row_len]
+ * forwards (row_len >= CHUNK_SIZE + STRIDE, rows * row_len <= the model's
+ * max_tokens), then each document's patches are emitted exactly as the chunk
+ * loop of process_document emits them (those starting before STRIDE twice
+ * when a document has more than one chunk).  Outputs are host memory:
+ * entropies / norms [total] indexed like the bytes; document d's patches are
+ * [patch_offsets[d], patch_offsets[d + 1]) of start / length / prominence /
+ * entropy, with starts inside the document.  total + STRIDE * n_docs entries
+ * always suffice; a smaller cap that is too small is BLT_ERR_SHAPE.  The
+ * handle's process_chunk state is untouched.  Waits for `stream`, then runs on
+ * the ingest driver's streams; returns when every output is written. */
+int blt_pipeline_process_documents(blt_pipeline* p, const uint8_t* bytes,
+                                   const int64_t* doc_offsets, int64_t n_docs, int32_t rows,
+                                   int32_t row_len, float* entropies, float* norms, int64_t cap,
+                                   int64_t* start, int64_t* length, float* prominence,
+                                   float* entropy, int64_t* patch_offsets, blt_stream_t stream);
+
 /* Synthetic inputs (host memory, deterministic across C and Python) ----- */
 
 /* splitmix64-seeded N(mean, std) samples (Box-Muller in double), as f32. */

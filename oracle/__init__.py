@@ -307,3 +307,79 @@ def process_document(cfg, weights, tokens, chunk, overlap, threshold, mode=0):
     coh = (N * N) / (H + np.float32(1e-6))
     return dict(entropies=H, norms=N, embeddings=E, coherence=coh.astype(np.float32),
                 starts=np.array(s[0], np.int32), lengths=np.array(ln[0], np.int32))
+
+
+def mean_f32(x, start, end):
+    """PipelineBuffer::compute_mean_prominence / compute_mean_entropy
+    (pipeline.rs:241-258): end clamped to len(x), start to end, 0 for an empty
+    span, else the left-to-right f32 sum over [start, end) divided by the
+    length as f32."""
+    end = min(end, len(x))
+    start = min(start, end)
+    if start >= end:
+        return np.float32(0)
+    s = np.add.accumulate(np.asarray(x[start:end], np.float32), dtype=np.float32)[-1]
+    return np.float32(s / np.float32(end - start))
+
+
+def pipeline_process_document(data, forward, threshold, chunk_size=4096, stride=2048):
+    """process_document (pipeline.rs:279-324) with PipelineBuffer::process_chunk
+    (pipeline.rs:111-238), stated step by step.
+
+    forward(tokens, start) -> (entropies, norms), f32 [n] each: the model on one
+    chunk, whose tokens are the raw byte values (no +4 offset, pipeline.rs:123)
+    and whose first byte is document position `start`.  chunk_size / stride are
+    the reference's CHUNK_SIZE / STRIDE (4096 / 2048; SAFE_ZONE_END = chunk_size
+    - stride); smaller values serve hand-worked cases.  Returns dict(patches=
+    [(start, length, prominence, entropy, bytes)], entropies, norms)."""
+    safe_zone_end = chunk_size - stride
+    data = bytes(data)
+    H = np.zeros(0, np.float32)
+    N = np.zeros(0, np.float32)
+    raw = b""
+    total_processed = 0
+    chunk_idx = 0
+    patches = []
+    total = len(data)
+    position = 0
+    while position < total:
+        chunk_end = min(position + chunk_size, total)
+        is_last = chunk_end >= total
+        actual_start = max(position - stride, 0) if position > 0 else 0
+        chunk = data[actual_start:chunk_end]
+        # ---- process_chunk ----
+        n = len(chunk)
+        chunk_start_absolute = total_processed
+        h, nn = forward(np.frombuffer(chunk, np.uint8).astype(np.int32), actual_start)
+        h = np.asarray(h, np.float32)
+        nn = np.asarray(nn, np.float32)
+        new_data_start = 0 if chunk_idx == 0 else stride
+        if chunk_idx == 0:
+            H, N, raw = np.concatenate([H, h]), np.concatenate([N, nn]), raw + chunk
+        elif new_data_start < n:
+            H = np.concatenate([H, h[new_data_start:]])
+            N = np.concatenate([N, nn[new_data_start:]])
+            raw = raw + chunk[new_data_start:]
+        acc = H.size
+        starts = patch_indices(patch_mask(H[None, :], threshold, 0))[0] if acc else []
+        cutoff = None if is_last else chunk_start_absolute + safe_zone_end
+        emit = []
+        for i, s in enumerate(starts):
+            if cutoff is None or s < cutoff:
+                end = starts[i + 1] if i + 1 < len(starts) else acc
+                if s >= max(total_processed - stride, 0) or chunk_idx == 0:
+                    emit.append((s, end))
+        for s, end in emit:
+            actual_end = min(end, len(raw))
+            patches.append((s, actual_end - s, mean_f32(N, s, actual_end),
+                            mean_f32(H, s, actual_end), raw[s:actual_end]))
+        if not is_last:
+            total_processed = chunk_start_absolute + max(n - stride, 0)
+        else:
+            total_processed = chunk_start_absolute + n
+        chunk_idx += 1
+        # ---- end of process_chunk ----
+        if is_last:
+            break
+        position = chunk_end
+    return dict(patches=patches, entropies=H, norms=N)
