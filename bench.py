@@ -152,6 +152,12 @@ def main():
                     help="config 5: documents go to the ingest driver in document-aligned "
                          "segments of about this many MiB (bounds host memory for the "
                          "outputs; one progress line per segment on stderr)")
+    ap.add_argument("--pipeline", action="store_true",
+                    help="measure the streaming pipeline of pipeline.rs instead (4096-byte "
+                         "chunks, 2048 context): the packed many-document form and the "
+                         "one-forward-per-chunk form over a prefix of the config-5 documents")
+    ap.add_argument("--pipeline-mib", type=float, default=8.0,
+                    help="--pipeline: MiB of the seeded document stream per pass")
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--seq", type=int, default=8192)
     ap.add_argument("--window", type=int, default=512)
@@ -203,6 +209,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
+    if args.pipeline:
+        bench_pipeline(args)
+        return
     if args.config == 5:
         bench_ingest(args)
         return
@@ -766,6 +775,111 @@ def bench_ingest(args):
                       "restatement (oracle: per-chunk forward, stitch, boundaries), %.1f s"
                       % (n_docs, done_bytes, c1 - c0),
             "parity_on_sample": {"entropy_max_abs": worst}}
+    print(json.dumps(result), flush=True)
+
+
+def bench_pipeline(args):
+    """The streaming pipeline (pipeline.rs:279-324) over a prefix of the config-5
+    document stream: raw bytes (no +4 offset), 4096-byte chunks with 2048 bytes
+    of context, the boundary pass over the accumulated entropies after each
+    chunk, per-patch means.  value = document bytes / second of the packed
+    many-document form (pipeline.process_documents: chunks of all documents as
+    segments of [rows, 8192] forwards); the one-forward-per-chunk form
+    (pipeline.process_document per document, as the reference runs it) is
+    reported beside it.  Host memory in and out."""
+    import numpy as np
+
+    from blt_burn_amd import model as M, pipeline as P, synth
+
+    steps = args.steps if args.steps is not None else 1
+    cfg = M.entropy_model_config()
+    F, D, V, L, H = 2048, cfg.dim, cfg.vocab_size, cfg.n_layers, cfg.resolved_n_heads()
+    B, T, W = args.batch, args.seq, args.window
+    seed = synth.config_seed(5)
+    weights = M.random_weights(cfg, seed, hidden=F)
+    model = M.LMTransformer(cfg, weights, device=0, max_tokens=B * T, window=W)
+    nbytes = int(args.pipeline_mib * 2 ** 20)
+    data, off = synth.documents(seed, nbytes)
+    docs = [data[off[i]:off[i + 1]].tobytes() for i in range(off.size - 1)]
+    wdata, woff = synth.documents(seed + 1, 2 ** 20)
+    wdocs = [wdata[woff[i]:woff[i + 1]].tobytes() for i in range(woff.size - 1)]
+    for _ in range(args.warmup):
+        P.process_documents(wdocs, model, args.threshold, rows=B, row_len=T)
+        for d in wdocs[:64]:
+            P.process_document(d, model, threshold=args.threshold)
+    model.read_profile()
+    model.set_profiling(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        packed = P.process_documents(docs, model, args.threshold, rows=B, row_len=T)
+    t1 = time.perf_counter()
+    prof = model.read_profile()
+    model.set_profiling(False)
+    sec = (t1 - t0) / steps
+    dom = "w13_gemm_silu"
+    ms_tot, launches = prof[dom]
+    per_launch_ms = ms_tot / launches
+    achieved = stage_flops(dom, B * T, B, T, D, F, V, H, W) / (per_launch_ms * 1e-3) / 1e12
+    gpu_ms = sum(ms for ms, n in prof.values()) / steps
+    c0 = time.perf_counter()
+    single = [P.process_document(d, model, threshold=args.threshold) for d in docs]
+    c1 = time.perf_counter()
+    n_patches = sum(len(r.patches) for r in packed)
+    worst = max(float(np.abs(a.entropies - b.entropies).max()) for a, b in zip(packed, single)
+                if a.entropies.size)
+    result = {
+        "metric": "document bytes/sec through the streaming pipeline (pipeline.rs "
+                  "process_document, BLT entropy model, bf16)",
+        "value": round(nbytes / sec, 1), "unit": "bytes/s", "n_gpus": 1, "steps": steps,
+        "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: %.1f MiB prefix of the seeded config-5 document stream (%d "
+                "documents), raw bytes as tokens, random-init bf16 weights"
+                % (nbytes / 2 ** 20, len(docs)),
+        "config": {"workload": "pipeline.rs: 4096-byte chunks with 2048 bytes of context, "
+                               "boundary pass over the accumulated entropies per chunk, "
+                               "per-patch means; chunks of all documents packed into "
+                               "[rows, row_len] forwards",
+                   "rows": B, "row_len": T, "window": W, "threshold": args.threshold},
+        "pipeline": {"patches_emitted": n_patches,
+                     "per_chunk_form_bytes_per_s": round(nbytes / (c1 - c0), 1),
+                     "per_chunk_form_s": round(c1 - c0, 3),
+                     "packed_vs_per_chunk_entropy_max_abs": worst,
+                     "gpu_model_ms": round(gpu_ms, 1),
+                     "gpu_model_busy_fraction": round(gpu_ms / (sec * 1e3), 4)},
+        "roofline": _with_achievable({"bound": "mfma", "kernel": dom,
+                                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                                      "unit": "TFLOP/s",
+                                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                                      "traffic": None, "launch_ms": round(per_launch_ms, 4)}),
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        import oracle  # the checker / CPU baseline only
+        cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+        os.environ["OMP_NUM_THREADS"] = str(cores)
+        oc = dict(dim=D, n_layers=L, n_heads=H, hidden=F, vocab=V, max_seqlen=cfg.max_seqlen,
+                  norm_eps=cfg.norm_eps, rope_theta=cfg.rope_theta, window=W)
+        ow = _oracle_weights(weights)
+
+        def fwd(tokens, start):
+            o = oracle.model_forward(oc, ow, tokens[None, :])
+            return o["entropies"][0], o["embedding_norms"][0]
+        n_docs, done_bytes, dH = 0, 0, 0.0
+        c0 = time.perf_counter()
+        while done_bytes < args.cpu_seq and n_docs < len(docs):
+            ref = oracle.pipeline_process_document(docs[n_docs], fwd, args.threshold)
+            dH = max(dH, float(np.abs(single[n_docs].entropies - ref["entropies"]).max()))
+            done_bytes += len(docs[n_docs])
+            n_docs += 1
+        c1 = time.perf_counter()
+        result["cpu_baseline"] = {
+            "value": round(done_bytes / (c1 - c0), 2), "unit": "bytes/s", "cores": cores,
+            "kind": "port",
+            "sample": "first %d documents (%d bytes) of the same stream through the oracle's "
+                      "restatement of process_document with the fp32 C forward, %.1f s"
+                      % (n_docs, done_bytes, c1 - c0),
+            "parity_on_sample": {"entropy_max_abs": dH}}
     print(json.dumps(result), flush=True)
 
 

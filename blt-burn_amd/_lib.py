@@ -67,6 +67,7 @@ EXPORTS = {
     "blt_pipeline_create": (c_i32, [c_vp, c_f64, c_vp]),
     "blt_pipeline_destroy": (c_i32, [c_vp]),
     "blt_pipeline_process_chunk": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_i64] + [c_vp] * 6),
+    "blt_pipeline_reset": (c_i32, [c_vp]),
     "blt_pipeline_accumulated": (c_i32, [c_vp, c_vp]),
     "blt_pipeline_read": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp]),
     "blt_pipeline_process_documents": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_vp,

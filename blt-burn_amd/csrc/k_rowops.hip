@@ -697,36 +697,109 @@ __global__ __launch_bounds__(PB_THREADS) void patch_boundary_kernel(
 // running to the row end; each sum runs left to right in f32 and is divided
 // by the patch length, as the reference's iter().sum::<f32>() / n does, so the
 // results are bit-identical to it.  Row layout as in patch_boundary_kernel;
-// starts and the outputs share the row offsets.  One block per row, one thread
-// per patch (patches are short; the rare long one only delays its own thread).
+// starts (ascending, as the boundary pass writes them) and the outputs share
+// the row offsets.
+//
+// One block per row walks it in tiles of PM_TILE positions staged in LDS with
+// coalesced loads.  Each patch that starts in a tile is one thread's serial
+// chain over the tile's LDS copy; the one patch that runs past the tile end
+// hands its partial sums (two LDS slots, alternating by tile) to thread 0 of
+// the next tile, which continues the same chain, so a patch of any length
+// costs LDS reads, not one dependent global load per element.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void patch_means_kernel(
+constexpr int PM_THREADS = 256;
+constexpr int PM_TILE = 2048;
+
+__global__ __launch_bounds__(PM_THREADS) void patch_means_kernel(
     const float* __restrict__ H, const float* __restrict__ N, const float* __restrict__ C,
     const int32_t* __restrict__ starts, const int32_t* __restrict__ count, int64_t T_dense,
     const int64_t* __restrict__ row_off, const int32_t* __restrict__ row_len,
     float* __restrict__ mH, float* __restrict__ mN, float* __restrict__ mC) {
+  __shared__ float sH[PM_TILE], sN[PM_TILE], sC[PM_TILE];
+  __shared__ float carry[2][3];  // partial sums handed to the next tile
+  __shared__ int32_t last[2];    // last patch started in the tile (atomicMax)
   const int64_t b = blockIdx.x;
   const int64_t roff = row_off ? row_off[b] : b * T_dense;
   const int64_t T = row_len ? (int64_t)row_len[b] : T_dense;
   int64_t n = count[b];
   n = n < 0 ? 0 : (n > T ? T : n);
-  for (int64_t p = threadIdx.x; p < n; p += blockDim.x) {
-    int64_t e = p + 1 < n ? (int64_t)starts[roff + p + 1] : T;
+  const int tid = threadIdx.x;
+  // patch p's span, clamped to 0 <= st <= e <= T
+  auto span = [&](int64_t p, int64_t& st, int64_t& e) {
+    e = p + 1 < n ? (int64_t)starts[roff + p + 1] : T;
     e = e < 0 ? 0 : (e > T ? T : e);
-    int64_t st = starts[roff + p];
+    st = starts[roff + p];
     st = st < 0 ? 0 : (st > e ? e : st);
-    float sh = 0.f, sn = 0.f, sc = 0.f;
-    for (int64_t t = st; t < e; ++t) {
-      sh += H[roff + t];
-      sn += N[roff + t];
-      if (C) sc += C[roff + t];
+  };
+  auto put = [&](int64_t p, float sh, float sn, float sc, int64_t len) {
+    const bool any = len > 0;
+    const float fl = (float)len;
+    if (mH) mH[roff + p] = any ? sh / fl : 0.f;
+    if (mN) mN[roff + p] = any ? sn / fl : 0.f;
+    if (mC) mC[roff + p] = any ? sc / fl : 0.f;
+  };
+  if (tid == 0) last[0] = -1;
+  int64_t p0 = 0;   // first patch that has not started in an earlier tile
+  int64_t cp = -1;  // patch continuing from the previous tile (-1: none)
+  int k = 0;
+  for (int64_t t0 = 0; t0 < T && (p0 < n || cp >= 0); t0 += PM_TILE, ++k) {
+    const int64_t t1 = t0 + PM_TILE < T ? t0 + PM_TILE : T;
+    const int w = (int)(t1 - t0);
+    for (int i = tid; i < w; i += PM_THREADS) {
+      sH[i] = H[roff + t0 + i];
+      sN[i] = N[roff + t0 + i];
+      if (C) sC[i] = C[roff + t0 + i];
     }
-    const float len = (float)(e - st);
-    const bool any = e > st;
-    if (mH) mH[roff + p] = any ? sh / len : 0.f;
-    if (mN) mN[roff + p] = any ? sn / len : 0.f;
-    if (mC) mC[roff + p] = any ? sc / len : 0.f;
+    __syncthreads();
+    // the next tile's counter, free since that tile's last read two syncs ago
+    if (tid == 0) last[(k + 1) & 1] = -1;
+    const int nc0 = cp >= 0 ? 1 : 0;  // chain 0 continues patch cp
+    for (int64_t j = tid;; j += PM_THREADS) {
+      int64_t p, st, e;
+      float sh = 0.f, sn = 0.f, sc = 0.f;
+      if (j < nc0) {
+        p = cp;
+        span(p, st, e);
+        sh = carry[k & 1][0];
+        sn = carry[k & 1][1];
+        sc = carry[k & 1][2];
+      } else {
+        p = p0 + (j - nc0);
+        if (p >= n) break;
+        span(p, st, e);
+        if (st >= t1) break;  // starts ascend: this and later patches start further on
+        atomicMax(&last[k & 1], (int32_t)p);
+      }
+      const int a = (int)((st > t0 ? st : t0) - t0);
+      const int z = (int)((e < t1 ? e : t1) - t0);
+#pragma unroll 8
+      for (int t = a; t < z; ++t) {
+        sh += sH[t];
+        sn += sN[t];
+        if (C) sc += sC[t];
+      }
+      if (e <= t1) {
+        put(p, sh, sn, sc, e - st);
+      } else {  // only the tile's last chain runs on
+        carry[(k + 1) & 1][0] = sh;
+        carry[(k + 1) & 1][1] = sn;
+        carry[(k + 1) & 1][2] = sc;
+      }
+    }
+    __syncthreads();
+    // block-uniform: the patches that started here and the chain that runs on
+    const int64_t lp = last[k & 1];
+    const int64_t lastchain = lp >= p0 ? lp : cp;
+    if (lp >= p0) p0 = lp + 1;
+    cp = -1;
+    if (lastchain >= 0) {
+      int64_t st, e;
+      span(lastchain, st, e);
+      if (e > t1) cp = lastchain;
+    }
   }
+  // patches that start at or past the row end (only for malformed starts)
+  for (int64_t p = p0 + tid; p < n; p += PM_THREADS) put(p, 0.f, 0.f, 0.f, 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1093,7 +1166,7 @@ int launch_patch_means(const float* H, const float* N, const float* C, const int
                        const int32_t* count, int64_t B, int64_t T, const int64_t* row_off,
                        const int32_t* row_len, float* mH, float* mN, float* mC, hipStream_t s) {
   if (B == 0) return 0;
-  hipLaunchKernelGGL(patch_means_kernel, dim3((unsigned)B), dim3(256), 0, s, H, N, C, starts,
+  hipLaunchKernelGGL(patch_means_kernel, dim3((unsigned)B), dim3(PM_THREADS), 0, s, H, N, C, starts,
                      count, T, row_off, row_len, mH, mN, mC);
   BLT_LAUNCH_CHECK("patch_means_kernel");
   return 0;

@@ -336,6 +336,7 @@ int Pipeline::process_documents(const uint8_t* bytes, const int64_t* doc_off, in
     int64_t slot, off;
   };
   std::vector<Clip> clips;
+  std::vector<float> span_H, span_N;
   int64_t span_n = 0;
   auto flush = [&]() -> int {
     if (clips.empty()) return 0;
@@ -344,8 +345,10 @@ int Pipeline::process_documents(const uint8_t* bytes, const int64_t* doc_off, in
     if ((r = v_H.reserve(b, s)) || (r = v_N.reserve(b, s)) || (r = v_starts.reserve(b, s)) ||
         (r = v_count.reserve(4, s)) || (r = v_mH.reserve(b, s)) || (r = v_mN.reserve(b, s)) ||
         (r = hv_starts.reserve(b)) || (r = hv_count.reserve(4)) || (r = hv_mH.reserve(b)) ||
-        (r = hv_mN.reserve(b)))
+        (r = hv_mN.reserve(b)) || (r = hv_H.reserve(b)) || (r = hv_N.reserve(b)))
       return r;
+    memcpy(hv_H.p, span_H.data(), b);
+    memcpy(hv_N.p, span_N.data(), b);
     int32_t* hs = hv_starts.as<int32_t>();
     for (size_t j = 0; j < clips.size(); ++j) hs[j] = (int32_t)clips[j].off;
     hv_count.as<int32_t>()[0] = (int32_t)clips.size();
@@ -367,6 +370,8 @@ int Pipeline::process_documents(const uint8_t* bytes, const int64_t* doc_off, in
       if (o_ent) o_ent[clips[j].slot] = hv_mH.as<float>()[j];
     }
     clips.clear();
+    span_H.clear();
+    span_N.clear();
     span_n = 0;
     return 0;
   };
@@ -386,20 +391,8 @@ int Pipeline::process_documents(const uint8_t* bytes, const int64_t* doc_off, in
       } else if (o_prom || o_ent) {
         const int64_t len = e - a;
         if (span_n + len > kSpanBatch && (err = flush())) return;
-        const size_t need = (size_t)(span_n + len) * 4;
-        if (need > hv_H.bytes) {
-          // grow the gathered spans, keeping what is already there
-          HostBuf nh, nn;
-          if ((err = nh.reserve(need)) || (err = nn.reserve(need))) return;
-          if (span_n) {
-            memcpy(nh.p, hv_H.p, (size_t)span_n * 4);
-            memcpy(nn.p, hv_N.p, (size_t)span_n * 4);
-          }
-          std::swap(hv_H.p, nh.p), std::swap(hv_H.bytes, nh.bytes);
-          std::swap(hv_N.p, nn.p), std::swap(hv_N.bytes, nn.bytes);
-        }
-        memcpy(hv_H.as<float>() + span_n, ent + base + a, (size_t)len * 4);
-        memcpy(hv_N.as<float>() + span_n, nrm + base + a, (size_t)len * 4);
+        span_H.insert(span_H.end(), ent + base + a, ent + base + e);
+        span_N.insert(span_N.end(), nrm + base + a, nrm + base + e);
         clips.push_back({w, span_n});
         span_n += len;
       }
@@ -441,6 +434,15 @@ int blt_pipeline_process_chunk(blt_pipeline* p, const uint8_t* chunk, int64_t n,
   reinterpret_cast<Pipeline*>(p)->s = reinterpret_cast<hipStream_t>(stream);
   return reinterpret_cast<Pipeline*>(p)->process_chunk(chunk, n, is_last != 0, cap, start, length,
                                                        prominence, entropy, n_patches);
+}
+
+int blt_pipeline_reset(blt_pipeline* p) {
+  if (!p) return fail(BLT_ERR_INVALID, "pipeline_reset: null handle");
+  Pipeline* q = reinterpret_cast<Pipeline*>(p);
+  q->acc_len = 0;
+  q->raw.clear();
+  q->total_processed = q->chunk_idx = q->next_patch_idx = 0;
+  return BLT_OK;
 }
 
 int blt_pipeline_accumulated(blt_pipeline* p, int64_t* len) {

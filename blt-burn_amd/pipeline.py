@@ -147,8 +147,11 @@ class PipelineBuffer:
 
 def process_document(data, entropy_model, blt_encoder=None, device=None, threshold=1.335):
     """pipeline.rs:279-324: the chunk loop over one document, one forward per
-    chunk through PipelineBuffer."""
-    buf = PipelineBuffer(threshold)
+    chunk through a PipelineBuffer (one kept per model and threshold, reset to
+    PipelineBuffer::new's state for every document, so its device and pinned
+    buffers are reused)."""
+    buf = _buffer_for(entropy_model, threshold)
+    check(_lib.lib().blt_pipeline_reset(buf._h), "blt_pipeline_reset")
     data = bytes(data)
     total = len(data)
     patches = []
@@ -162,9 +165,6 @@ def process_document(data, entropy_model, blt_encoder=None, device=None, thresho
         if is_last:
             break
         pos = chunk_end
-    if buf._h is None:  # an empty document never ran a chunk
-        z = np.zeros(0, np.float32)
-        return ProcessingResult(patches=[], entropies=z, norms=z.copy())
     H, N, _ = buf._read(0, buf.accumulated())
     return ProcessingResult(patches=patches, entropies=H, norms=N)
 
@@ -191,7 +191,7 @@ def process_documents(docs, entropy_model, threshold=1.335, rows=None, row_len=8
     prom = np.zeros(max(cap, 1), np.float32)
     ent = np.zeros(max(cap, 1), np.float32)
     poff = np.zeros(len(docs) + 1, np.int64)
-    h = _handle_for(entropy_model, threshold)
+    h = _buffer_for(entropy_model, threshold)._h
     check(_lib.lib().blt_pipeline_process_documents(
         h, _ptr(flat), off.ctypes.data, len(docs), rows, row_len, H.ctypes.data, N.ctypes.data,
         cap, start.ctypes.data, length.ctypes.data, prom.ctypes.data, ent.ctypes.data,
@@ -206,9 +206,10 @@ def process_documents(docs, entropy_model, threshold=1.335, rows=None, row_len=8
     return out
 
 
-def _handle_for(model, threshold):
-    """One blt_pipeline handle per (model, threshold) for process_documents,
-    kept on the model (its ingest buffers are reused by later calls)."""
+def _buffer_for(model, threshold):
+    """The PipelineBuffer that process_document and process_documents use for
+    this model and threshold, kept on the model (its device, pinned and ingest
+    buffers are reused by later calls)."""
     cache = model.__dict__.setdefault("_pipeline_cache", {})
     key = float(threshold)
     buf = cache.get(key)
@@ -216,7 +217,7 @@ def _handle_for(model, threshold):
         buf = PipelineBuffer(threshold)
         buf._bind(model)
         cache[key] = buf
-    return buf._h
+    return buf
 
 
 __all__ = ["CHUNK_SIZE", "STRIDE", "SAFE_ZONE_END", "PatchData", "ProcessingResult",

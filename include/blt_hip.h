@@ -427,6 +427,9 @@ int blt_pipeline_destroy(blt_pipeline* p);
 int blt_pipeline_process_chunk(blt_pipeline* p, const uint8_t* chunk, int64_t n, int32_t is_last,
                                int64_t cap, int64_t* start, int64_t* length, float* prominence,
                                float* entropy, int64_t* n_patches, blt_stream_t stream);
+/* Back to the state of PipelineBuffer::new (nothing accumulated, chunk 0
+ * next), keeping the handle's buffers for the next document. */
+int blt_pipeline_reset(blt_pipeline* p);
 /* Number of accumulated positions (PipelineBuffer::entropies().len()). */
 int blt_pipeline_accumulated(blt_pipeline* p, int64_t* len);
 /* PipelineBuffer::entropies / norms / raw_bytes (pipeline.rs:260-273): copies

@@ -107,6 +107,35 @@ def test_device_bit_exact_vs_oracle():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("T", [5000, 8192, 20000])
+def test_device_long_patches_bit_exact(T):
+    """Patches longer than the kernel's 2048-position LDS tiles (their sums
+    carried from tile to tile), patches ending or starting exactly on tile
+    edges, and one patch over the whole row, bit-exact against the oracle."""
+    import torch
+    from blt_burn_amd import patcher
+    rng = np.random.default_rng(T)
+    rows = [[0], [0, 1], [0, 2047, 2048, 2049, 4095, 4096, 4097],
+            [0, 1, 3000, T - 1], [0] + sorted(rng.choice(np.arange(1, T), 7, replace=False)
+                                              .tolist()),
+            [0] + sorted(rng.choice(np.arange(1, T), T // 3, replace=False).tolist())]
+    B = len(rows)
+    H = rng.normal(3.0, 1.0, (B, T)).astype(np.float32)
+    N = (rng.random((B, T)) * 30).astype(np.float32)
+    C = (N * N / (H + 1e-6)).astype(np.float32)
+    st, ct = _starts(rows, T)
+    mH, mN, mC = patcher.patch_means(torch.from_numpy(H).cuda(), torch.from_numpy(N).cuda(),
+                                     torch.from_numpy(st).cuda(), torch.from_numpy(ct).cuda(),
+                                     torch.from_numpy(C).cuda())
+    rH, rN, rC = oracle.patch_means(H, N, st, ct, C)
+    for b in range(B):
+        n = ct[b]
+        assert np.array_equal(mH.cpu().numpy()[b, :n], rH[b, :n]), (T, b)
+        assert np.array_equal(mN.cpu().numpy()[b, :n], rN[b, :n]), (T, b)
+        assert np.array_equal(mC.cpu().numpy()[b, :n], rC[b, :n]), (T, b)
+
+
+@pytest.mark.gpu
 def test_device_rejects_bad_out_tensors():
     import torch
     from blt_burn_amd import BltError, patcher
