@@ -714,29 +714,32 @@ __global__ __launch_bounds__(PM_THREADS) void patch_means_kernel(
     const float* __restrict__ H, const float* __restrict__ N, const float* __restrict__ C,
     const int32_t* __restrict__ starts, const int32_t* __restrict__ count, int64_t T_dense,
     const int64_t* __restrict__ row_off, const int32_t* __restrict__ row_len,
-    float* __restrict__ mH, float* __restrict__ mN, float* __restrict__ mC) {
+    float* __restrict__ mH, float* __restrict__ mN, float* __restrict__ mC,
+    const int64_t* __restrict__ out_off) {
   __shared__ float sH[PM_TILE], sN[PM_TILE], sC[PM_TILE];
   __shared__ float carry[2][3];  // partial sums handed to the next tile
   __shared__ int32_t last[2];    // last patch started in the tile (atomicMax)
   const int64_t b = blockIdx.x;
   const int64_t roff = row_off ? row_off[b] : b * T_dense;
   const int64_t T = row_len ? (int64_t)row_len[b] : T_dense;
-  int64_t n = count[b];
+  const int64_t ooff = out_off ? out_off[b] : roff;
+  // without starts every row is one patch [0, T)
+  int64_t n = starts ? (int64_t)count[b] : 1;
   n = n < 0 ? 0 : (n > T ? T : n);
   const int tid = threadIdx.x;
   // patch p's span, clamped to 0 <= st <= e <= T
   auto span = [&](int64_t p, int64_t& st, int64_t& e) {
     e = p + 1 < n ? (int64_t)starts[roff + p + 1] : T;
     e = e < 0 ? 0 : (e > T ? T : e);
-    st = starts[roff + p];
+    st = starts ? (int64_t)starts[roff + p] : 0;
     st = st < 0 ? 0 : (st > e ? e : st);
   };
   auto put = [&](int64_t p, float sh, float sn, float sc, int64_t len) {
     const bool any = len > 0;
     const float fl = (float)len;
-    if (mH) mH[roff + p] = any ? sh / fl : 0.f;
-    if (mN) mN[roff + p] = any ? sn / fl : 0.f;
-    if (mC) mC[roff + p] = any ? sc / fl : 0.f;
+    if (mH) mH[ooff + p] = any ? sh / fl : 0.f;
+    if (mN) mN[ooff + p] = any ? sn / fl : 0.f;
+    if (mC) mC[ooff + p] = any ? sc / fl : 0.f;
   };
   if (tid == 0) last[0] = -1;
   int64_t p0 = 0;   // first patch that has not started in an earlier tile
@@ -1164,10 +1167,11 @@ int launch_patch_boundaries_varlen(const float* H, const int64_t* row_off, const
 
 int launch_patch_means(const float* H, const float* N, const float* C, const int32_t* starts,
                        const int32_t* count, int64_t B, int64_t T, const int64_t* row_off,
-                       const int32_t* row_len, float* mH, float* mN, float* mC, hipStream_t s) {
+                       const int32_t* row_len, float* mH, float* mN, float* mC, hipStream_t s,
+                       const int64_t* out_off) {
   if (B == 0) return 0;
   hipLaunchKernelGGL(patch_means_kernel, dim3((unsigned)B), dim3(PM_THREADS), 0, s, H, N, C, starts,
-                     count, T, row_off, row_len, mH, mN, mC);
+                     count, T, row_off, row_len, mH, mN, mC, out_off);
   BLT_LAUNCH_CHECK("patch_means_kernel");
   return 0;
 }

@@ -113,8 +113,8 @@ struct Pipeline {
   HostBuf h_tok;
   DevBuf d_tok, c_H, c_N;
   // boundary pass and means of an accumulated suffix (or of clipped spans)
-  DevBuf v_H, v_N, v_starts, v_lens, v_count, v_mH, v_mN;
-  HostBuf hv_starts, hv_count, hv_mH, hv_mN, hv_H, hv_N;
+  DevBuf v_H, v_N, v_starts, v_lens, v_count, v_mH, v_mN, v_off;
+  HostBuf hv_starts, hv_count, hv_mH, hv_mN, hv_H, hv_N, hv_off;
   // the batched form's ingest driver
   blt_ingest* ing = nullptr;
   int32_t ing_rows = 0, ing_row_len = 0;
@@ -340,32 +340,40 @@ int Pipeline::process_documents(const uint8_t* bytes, const int64_t* doc_off, in
   int64_t span_n = 0;
   auto flush = [&]() -> int {
     if (clips.empty()) return 0;
+    // one row (one block) per clipped span, its mean written to slot j
+    const size_t nc = clips.size();
     const size_t b = (size_t)span_n * 4;
     int r;
-    if ((r = v_H.reserve(b, s)) || (r = v_N.reserve(b, s)) || (r = v_starts.reserve(b, s)) ||
-        (r = v_count.reserve(4, s)) || (r = v_mH.reserve(b, s)) || (r = v_mN.reserve(b, s)) ||
-        (r = hv_starts.reserve(b)) || (r = hv_count.reserve(4)) || (r = hv_mH.reserve(b)) ||
-        (r = hv_mN.reserve(b)) || (r = hv_H.reserve(b)) || (r = hv_N.reserve(b)))
+    if ((r = v_H.reserve(b, s)) || (r = v_N.reserve(b, s)) || (r = v_mH.reserve(nc * 4, s)) ||
+        (r = v_mN.reserve(nc * 4, s)) || (r = v_off.reserve(nc * 16, s)) ||
+        (r = v_lens.reserve(nc * 4, s)) || (r = hv_H.reserve(b)) || (r = hv_N.reserve(b)) ||
+        (r = hv_off.reserve(nc * 16)) || (r = hv_starts.reserve(nc * 4)) ||
+        (r = hv_mH.reserve(nc * 4)) || (r = hv_mN.reserve(nc * 4)))
       return r;
     memcpy(hv_H.p, span_H.data(), b);
     memcpy(hv_N.p, span_N.data(), b);
-    int32_t* hs = hv_starts.as<int32_t>();
-    for (size_t j = 0; j < clips.size(); ++j) hs[j] = (int32_t)clips[j].off;
-    hv_count.as<int32_t>()[0] = (int32_t)clips.size();
+    int64_t* ho = hv_off.as<int64_t>();  // [nc] span offsets, then [nc] output slots
+    int32_t* hl = hv_starts.as<int32_t>();
+    for (size_t j = 0; j < nc; ++j) {
+      const int64_t end = j + 1 < nc ? clips[j + 1].off : span_n;
+      ho[j] = clips[j].off;
+      ho[nc + j] = (int64_t)j;
+      hl[j] = (int32_t)(end - clips[j].off);
+    }
     BLT_HIP_CHECK(hipSetDevice(m->device));
     BLT_HIP_CHECK(hipMemcpyAsync(v_H.p, hv_H.p, b, hipMemcpyHostToDevice, s));
     BLT_HIP_CHECK(hipMemcpyAsync(v_N.p, hv_N.p, b, hipMemcpyHostToDevice, s));
-    BLT_HIP_CHECK(hipMemcpyAsync(v_starts.p, hv_starts.p, clips.size() * 4,
-                                 hipMemcpyHostToDevice, s));
-    BLT_HIP_CHECK(hipMemcpyAsync(v_count.p, hv_count.p, 4, hipMemcpyHostToDevice, s));
-    if ((r = launch_patch_means(v_H.as<float>(), v_N.as<float>(), nullptr, v_starts.as<int32_t>(),
-                                v_count.as<int32_t>(), 1, span_n, nullptr, nullptr,
-                                v_mH.as<float>(), v_mN.as<float>(), nullptr, s)))
+    BLT_HIP_CHECK(hipMemcpyAsync(v_off.p, hv_off.p, nc * 16, hipMemcpyHostToDevice, s));
+    BLT_HIP_CHECK(hipMemcpyAsync(v_lens.p, hv_starts.p, nc * 4, hipMemcpyHostToDevice, s));
+    const int64_t* d_off = v_off.as<int64_t>();
+    if ((r = launch_patch_means(v_H.as<float>(), v_N.as<float>(), nullptr, nullptr, nullptr,
+                                (int64_t)nc, 0, d_off, v_lens.as<int32_t>(), v_mH.as<float>(),
+                                v_mN.as<float>(), nullptr, s, d_off + nc)))
       return r;
-    BLT_HIP_CHECK(hipMemcpyAsync(hv_mH.p, v_mH.p, clips.size() * 4, hipMemcpyDeviceToHost, s));
-    BLT_HIP_CHECK(hipMemcpyAsync(hv_mN.p, v_mN.p, clips.size() * 4, hipMemcpyDeviceToHost, s));
+    BLT_HIP_CHECK(hipMemcpyAsync(hv_mH.p, v_mH.p, nc * 4, hipMemcpyDeviceToHost, s));
+    BLT_HIP_CHECK(hipMemcpyAsync(hv_mN.p, v_mN.p, nc * 4, hipMemcpyDeviceToHost, s));
     BLT_HIP_CHECK(hipStreamSynchronize(s));
-    for (size_t j = 0; j < clips.size(); ++j) {
+    for (size_t j = 0; j < nc; ++j) {
       if (o_prom) o_prom[clips[j].slot] = hv_mN.as<float>()[j];
       if (o_ent) o_ent[clips[j].slot] = hv_mH.as<float>()[j];
     }

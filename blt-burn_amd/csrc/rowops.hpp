@@ -34,10 +34,14 @@ int launch_patch_boundaries(const float* H, int64_t B, int64_t T, float thr, int
                             hipStream_t s);
 
 // per-patch means of H / N / C over the patches starts[0 .. count) of each row
-// (row_off / row_len NULL: dense rows of T); C, mH, mN, mC may be NULL
+// (row_off / row_len NULL: dense rows of T); C, mH, mN, mC may be NULL.
+// starts NULL: each row is one patch over the whole row (count unused).
+// out_off (optional): row b's means go to m*[out_off[b] + p] instead of the
+// row's own offset.
 int launch_patch_means(const float* H, const float* N, const float* C, const int32_t* starts,
                        const int32_t* count, int64_t B, int64_t T, const int64_t* row_off,
-                       const int32_t* row_len, float* mH, float* mN, float* mC, hipStream_t s);
+                       const int32_t* row_len, float* mH, float* mN, float* mC, hipStream_t s,
+                       const int64_t* out_off = nullptr);
 
 int launch_scatter_tokens(const int32_t* dest, const float* H, const float* N, const float* C,
                           float* Ho, float* No, float* Co, int64_t n, hipStream_t s);
