@@ -96,3 +96,42 @@ def test_pipeline_closed_form(L, sparse):
     for s, n, p, h, b in r["patches"]:
         assert b == data[s:s + n] and n >= 1
     np.testing.assert_array_equal(r["entropies"], H)
+
+
+def _closed_form_general(H, thr, C, S):
+    """The emitted (start, end) pairs for chunk C and stride S <= C, from the
+    chunk geometry: chunk 0 keeps [0, C) and confirms starts below C - S (all
+    when it is the last); chunk k >= 1 starts at kC - S, keeps [kC, (k + 1)C)
+    and confirms starts in [max(kC - 2S, 0), (k + 1)C - 2S) (no upper end for
+    the last chunk); every end is clipped at the accumulated end."""
+    L = H.size
+    S_ = oracle.patch_indices(oracle.patch_mask(H[None, :], thr, 0))[0] if L else []
+    nxt = {s: (S_[i + 1] if i + 1 < len(S_) else L) for i, s in enumerate(S_)}
+    out = []
+    k = 0
+    while k * C < L or (k == 0 and L > 0):
+        acc = min((k + 1) * C, L)
+        last = (k + 1) * C >= L
+        lo = 0 if k == 0 else max(k * C - 2 * S, 0)
+        hi = None if last else ((C - S) if k == 0 else (k + 1) * C - 2 * S)
+        out += [(s, min(nxt[s], acc)) for s in S_
+                if s >= lo and (hi is None or s < hi) and s < acc]
+        if last:
+            break
+        k += 1
+    return out
+
+
+def test_pipeline_closed_form_any_chunking():
+    rng = np.random.default_rng(77)
+    for _ in range(400):
+        C = int(rng.integers(2, 13))
+        S = int(rng.integers(1, C + 1))
+        L = int(rng.integers(0, 70))
+        H = (rng.integers(0, 4, size=L) * rng.choice([0.0, 1.0, 2.5], size=L)).astype(np.float32)
+        N = rng.uniform(0.5, 2.0, size=L).astype(np.float32)
+        data = rng.integers(0, 256, size=L, dtype=np.uint8).tobytes()
+        r = oracle.pipeline_process_document(data, _table_forward(H, N, data), 1.0, C, S)
+        got = [(s, s + n) for s, n, *_ in r["patches"]]
+        assert got == _closed_form_general(H, 1.0, C, S), (C, S, L)
+        np.testing.assert_array_equal(r["entropies"], H)
