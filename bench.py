@@ -195,7 +195,8 @@ def main():
         return
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(rows shard with no collective; see DESIGN.md). Run with --gpus 1.",
+              "(rows and documents are independent, so more GPUs would each take a "
+              "share of them with no collective). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
 
