@@ -322,9 +322,66 @@ def mean_f32(x, start, end):
     return np.float32(s / np.float32(end - start))
 
 
+class PipelineBuffer:
+    """PipelineBuffer (pipeline.rs:74-274) stated step by step; chunk_size /
+    stride as in pipeline_process_document."""
+
+    def __init__(self, threshold, chunk_size=4096, stride=2048):
+        self.threshold = threshold
+        self.stride = stride
+        self.safe_zone_end = chunk_size - stride
+        self.entropies = np.zeros(0, np.float32)
+        self.norms = np.zeros(0, np.float32)
+        self.raw = b""
+        self.total_processed = 0
+        self.chunk_idx = 0
+
+    def process_chunk(self, chunk, forward, is_last):
+        """pipeline.rs:111-238.  forward(tokens, start) -> (entropies, norms) of the
+        model on this chunk, where start is the accumulated position of the
+        chunk's first byte (its kept outputs land from position start +
+        new_data_start on).  Returns [(start, length, prominence, entropy, bytes)]."""
+        chunk = bytes(chunk)
+        n = len(chunk)
+        chunk_start_absolute = self.total_processed
+        new_data_start = 0 if self.chunk_idx == 0 else self.stride
+        h, nn = forward(np.frombuffer(chunk, np.uint8).astype(np.int32),
+                        self.entropies.size - new_data_start)
+        h = np.asarray(h, np.float32)
+        nn = np.asarray(nn, np.float32)
+        if self.chunk_idx == 0:
+            self.entropies = np.concatenate([self.entropies, h])
+            self.norms = np.concatenate([self.norms, nn])
+            self.raw = self.raw + chunk
+        elif new_data_start < n:
+            self.entropies = np.concatenate([self.entropies, h[new_data_start:]])
+            self.norms = np.concatenate([self.norms, nn[new_data_start:]])
+            self.raw = self.raw + chunk[new_data_start:]
+        acc = self.entropies.size
+        starts = patch_indices(patch_mask(self.entropies[None, :], self.threshold, 0))[0] \
+            if acc else []
+        cutoff = None if is_last else chunk_start_absolute + self.safe_zone_end
+        emit = []
+        for i, s in enumerate(starts):
+            if cutoff is None or s < cutoff:
+                end = starts[i + 1] if i + 1 < len(starts) else acc
+                if s >= max(self.total_processed - self.stride, 0) or self.chunk_idx == 0:
+                    emit.append((s, end))
+        out = []
+        for s, end in emit:
+            actual_end = min(end, len(self.raw))
+            out.append((s, actual_end - s, mean_f32(self.norms, s, actual_end),
+                        mean_f32(self.entropies, s, actual_end), self.raw[s:actual_end]))
+        if not is_last:
+            self.total_processed = chunk_start_absolute + max(n - self.stride, 0)
+        else:
+            self.total_processed = chunk_start_absolute + n
+        self.chunk_idx += 1
+        return out
+
+
 def pipeline_process_document(data, forward, threshold, chunk_size=4096, stride=2048):
-    """process_document (pipeline.rs:279-324) with PipelineBuffer::process_chunk
-    (pipeline.rs:111-238), stated step by step.
+    """process_document (pipeline.rs:279-324) over PipelineBuffer.process_chunk.
 
     forward(tokens, start) -> (entropies, norms), f32 [n] each: the model on one
     chunk, whose tokens are the raw byte values (no +4 offset, pipeline.rs:123)
@@ -332,13 +389,8 @@ def pipeline_process_document(data, forward, threshold, chunk_size=4096, stride=
     the reference's CHUNK_SIZE / STRIDE (4096 / 2048; SAFE_ZONE_END = chunk_size
     - stride); smaller values serve hand-worked cases.  Returns dict(patches=
     [(start, length, prominence, entropy, bytes)], entropies, norms)."""
-    safe_zone_end = chunk_size - stride
+    buf = PipelineBuffer(threshold, chunk_size, stride)
     data = bytes(data)
-    H = np.zeros(0, np.float32)
-    N = np.zeros(0, np.float32)
-    raw = b""
-    total_processed = 0
-    chunk_idx = 0
     patches = []
     total = len(data)
     position = 0
@@ -346,40 +398,8 @@ def pipeline_process_document(data, forward, threshold, chunk_size=4096, stride=
         chunk_end = min(position + chunk_size, total)
         is_last = chunk_end >= total
         actual_start = max(position - stride, 0) if position > 0 else 0
-        chunk = data[actual_start:chunk_end]
-        # ---- process_chunk ----
-        n = len(chunk)
-        chunk_start_absolute = total_processed
-        h, nn = forward(np.frombuffer(chunk, np.uint8).astype(np.int32), actual_start)
-        h = np.asarray(h, np.float32)
-        nn = np.asarray(nn, np.float32)
-        new_data_start = 0 if chunk_idx == 0 else stride
-        if chunk_idx == 0:
-            H, N, raw = np.concatenate([H, h]), np.concatenate([N, nn]), raw + chunk
-        elif new_data_start < n:
-            H = np.concatenate([H, h[new_data_start:]])
-            N = np.concatenate([N, nn[new_data_start:]])
-            raw = raw + chunk[new_data_start:]
-        acc = H.size
-        starts = patch_indices(patch_mask(H[None, :], threshold, 0))[0] if acc else []
-        cutoff = None if is_last else chunk_start_absolute + safe_zone_end
-        emit = []
-        for i, s in enumerate(starts):
-            if cutoff is None or s < cutoff:
-                end = starts[i + 1] if i + 1 < len(starts) else acc
-                if s >= max(total_processed - stride, 0) or chunk_idx == 0:
-                    emit.append((s, end))
-        for s, end in emit:
-            actual_end = min(end, len(raw))
-            patches.append((s, actual_end - s, mean_f32(N, s, actual_end),
-                            mean_f32(H, s, actual_end), raw[s:actual_end]))
-        if not is_last:
-            total_processed = chunk_start_absolute + max(n - stride, 0)
-        else:
-            total_processed = chunk_start_absolute + n
-        chunk_idx += 1
-        # ---- end of process_chunk ----
+        patches += buf.process_chunk(data[actual_start:chunk_end], forward, is_last)
         if is_last:
             break
         position = chunk_end
-    return dict(patches=patches, entropies=H, norms=N)
+    return dict(patches=patches, entropies=buf.entropies, norms=buf.norms)

@@ -199,3 +199,48 @@ def test_pipeline_entropy_model():
     print("pipeline at real dims: %d documents (%d bytes), packed vs separate entropy "
           "max|d|=%.2e" % (len(docs), sum(map(len, docs)), worst))
     torch.cuda.synchronize()
+
+
+def _replay_at(H, N):
+    """Model outputs for a chunk whose first byte sits at accumulated position
+    `start` (negative for the dropped context of an odd call sequence): the
+    accumulated values where they exist, zeros elsewhere (never kept)."""
+    def fwd(tokens, start):
+        n = tokens.size
+        h = np.zeros(n, np.float32)
+        m = np.zeros(n, np.float32)
+        lo, hi = max(start, 0), min(start + n, H.size)
+        if hi > lo:
+            h[lo - start:hi - start] = H[lo:hi]
+            m[lo - start:hi - start] = N[lo:hi]
+        return h, m
+    return fwd
+
+
+@pytest.mark.parametrize("calls", [
+    [(3000, False), (100, False), (5000, False), (0, False), (2049, False), (700, True)],
+    [(0, False), (10, False), (4096, True)],
+    [(4000, True), (3000, False), (2500, True)],
+    [(1, False), (2, False), (2048, False), (2050, False), (6144, False), (9, True)],
+])
+def test_pipeline_direct_chunk_calls_tiny(calls):
+    """process_chunk called directly with chunks of any size (shorter than the
+    context, empty, calls after a last chunk): every call's patches equal the
+    oracle's PipelineBuffer on the same accumulated signals, bit for bit."""
+    cfg = M.LMTransformerConfig(**TINY)
+    w = M.random_weights(cfg, 45, hidden=256)
+    m = M.LMTransformer(cfg, w, device=0, max_tokens=8192, window=0)
+    rng = np.random.default_rng(len(calls))
+    chunks = [synth.documents(int(rng.integers(1 << 30)), n)[0].tobytes() if n else b""
+              for n, _ in calls]
+    buf = P.PipelineBuffer(THR)
+    got = [buf.process_chunk(c, m, None, None, last) for c, (_, last) in zip(chunks, calls)]
+    H, N = buf.entropies(), buf.norms()
+    ref = oracle.PipelineBuffer(THR)
+    fwd = _replay_at(H, N)
+    raw = buf.raw_bytes()
+    for c, (_, last), g in zip(chunks, calls, got):
+        want = ref.process_chunk(c, fwd, last)
+        _assert_patches_exact(g, want, raw)
+    np.testing.assert_array_equal(ref.entropies, H)
+    assert ref.raw == raw
