@@ -73,6 +73,9 @@ class PipelineBuffer:
 
     def _bind(self, model):
         if self._h is None:
+            if model is None or not hasattr(model, "_h"):
+                raise BltError("PipelineBuffer.process_chunk needs the entropy model (an "
+                               "LMTransformer) on its first call")
             h = ctypes.c_void_p()
             check(_lib.lib().blt_pipeline_create(model._h, self.threshold, ctypes.byref(h)),
                   "blt_pipeline_create")

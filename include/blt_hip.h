@@ -423,7 +423,9 @@ int blt_pipeline_destroy(blt_pipeline* p);
  * lower / cutoff are the reference's confirmation window, so cap >= the
  * accumulated length after the call always suffices (BLT_ERR_SHAPE before
  * any work otherwise).  The work runs on `stream` (ordered after the caller's
- * earlier work there); returns when every output is written. */
+ * earlier work there); returns when every output is written.  A call that
+ * fails after its forward (a HIP error) may leave the handle part-way through
+ * the chunk: blt_pipeline_reset it before the next document. */
 int blt_pipeline_process_chunk(blt_pipeline* p, const uint8_t* chunk, int64_t n, int32_t is_last,
                                int64_t cap, int64_t* start, int64_t* length, float* prominence,
                                float* entropy, int64_t* n_patches, blt_stream_t stream);
