@@ -359,7 +359,9 @@ def _attn_case(B, H, T, causal, window, theta, seed=30):
 @pytest.mark.parametrize("B,H,T,causal,window,theta", [
     (1, 2, 64, True, 0, 0.0), (2, 3, 200, True, 0, 0.0), (1, 2, 333, True, 64, 0.0),
     (1, 1, 130, False, 0, 0.0), (1, 2, 300, True, 0, 10000.0), (2, 2, 700, True, 512, 10000.0),
-    (1, 1, 1, True, 0, 10000.0), (1, 1, 97, True, 1, 0.0)])
+    (1, 1, 1, True, 0, 10000.0), (1, 1, 97, True, 1, 0.0),
+    # RoPE slices of uneven size: 3 batch slices; 4 head slices of 5 heads
+    (3, 2, 300, True, 64, 10000.0), (1, 5, 200, True, 0, 10000.0)])
 def test_attention_vs_oracle(B, H, T, causal, window, theta):
     o, ref = _attn_case(B, H, T, causal, window, theta)
     # bf16 operands and bf16 P in the PV product: |err| <= 2e-2 for N(0,1) inputs
