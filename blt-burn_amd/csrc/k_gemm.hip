@@ -85,7 +85,16 @@ int launch_gemm(const GemmArgs& a_in, hipStream_t s) {
   const int64_t two31 = int64_t(1) << 31;
   const bool fits = 256 * (a.lda > a.ldb ? a.lda : a.ldb) * 2 + a.K * 2 < two31 &&
                     256 * a.ldc * 4 < two31;
-  if (a.N % 256 == 0 && fits) return run_gemm_dma_epi<256, 256, 64, 2, 4>(a, s);
+  if (a.N % 256 == 0 && fits) {
+    // Fewer 256x256 tiles than CUs (a single document's forward, e.g. the
+    // 768-wide projections at a few thousand rows): the same kernel on 128x128
+    // tiles over 2x2 waves.  The wave tile keeps its 64 columns, the K order
+    // per output and the per-64-column norm partials, so every output is
+    // bit-identical to the 256x256 launch's.
+    const int64_t nb256 = ((a.M + 255) / 256) * (a.N / 256);
+    if (nb256 < device_cus()) return run_gemm_dma_epi<128, 128, 64, 2, 2>(a, s);
+    return run_gemm_dma_epi<256, 256, 64, 2, 4>(a, s);
+  }
   return run_gemm<128, 128, 32, 2, 2, 2, 3>(a, s);
 }
 
