@@ -28,15 +28,42 @@ SAFE_ZONE_END = CHUNK_SIZE - STRIDE
 EMBEDDING_DIM = 768
 
 
-@dataclass
 class PatchData:
-    """pipeline.rs:46-60."""
-    start_offset: int
-    length: int
-    embedding: np.ndarray  # f32 [768], zeros as the reference emits them
-    prominence: float
-    entropy: float
-    bytes: bytes
+    """pipeline.rs:46-60.  embedding is an f32 [768] zero vector of its own, as
+    the reference emits it; it is allocated on first access (most callers read
+    only the offsets, means and bytes, and a document yields hundreds of patches)."""
+    __slots__ = ("start_offset", "length", "_embedding", "prominence", "entropy", "bytes")
+
+    def __init__(self, start_offset, length, embedding=None, prominence=0.0, entropy=0.0,
+                 bytes=b""):
+        self.start_offset = start_offset
+        self.length = length
+        self._embedding = embedding
+        self.prominence = prominence
+        self.entropy = entropy
+        self.bytes = bytes
+
+    @property
+    def embedding(self) -> np.ndarray:
+        if self._embedding is None:
+            self._embedding = np.zeros(EMBEDDING_DIM, np.float32)
+        return self._embedding
+
+    @embedding.setter
+    def embedding(self, value):
+        self._embedding = value
+
+    def __eq__(self, other):
+        if not isinstance(other, PatchData):
+            return NotImplemented
+        return (self.start_offset == other.start_offset and self.length == other.length and
+                self.prominence == other.prominence and self.entropy == other.entropy and
+                self.bytes == other.bytes and
+                np.array_equal(self.embedding, other.embedding))
+
+    def __repr__(self):
+        return ("PatchData(start_offset=%d, length=%d, prominence=%r, entropy=%r, bytes=%r)"
+                % (self.start_offset, self.length, self.prominence, self.entropy, self.bytes))
 
 
 @dataclass
@@ -52,13 +79,11 @@ def _ptr(a):
 
 
 def _patches(starts, lengths, prom, ent, raw, base=0):
-    out = []
-    for a, n, p, h in zip(starts.tolist(), lengths.tolist(), prom.tolist(), ent.tolist()):
-        out.append(PatchData(start_offset=a, length=n,
-                             embedding=np.zeros(EMBEDDING_DIM, np.float32),
-                             prominence=p, entropy=h,
-                             bytes=bytes(raw[base + a:base + a + n])))
-    return out
+    # raw is one document or chunk window (small): one bytes copy, then slices
+    if not isinstance(raw, bytes):
+        raw = bytes(raw)
+    return [PatchData(a, n, None, p, h, raw[base + a:base + a + n])
+            for a, n, p, h in zip(starts.tolist(), lengths.tolist(), prom.tolist(), ent.tolist())]
 
 
 class PipelineBuffer:
@@ -204,7 +229,7 @@ def process_documents(docs, entropy_model, threshold=1.335, rows=None, row_len=8
         a, b = int(off[d]), int(off[d + 1])
         p, q = int(poff[d]), int(poff[d + 1])
         out.append(ProcessingResult(
-            patches=_patches(start[p:q], length[p:q], prom[p:q], ent[p:q], flat, base=a),
+            patches=_patches(start[p:q], length[p:q], prom[p:q], ent[p:q], docs[d]),
             entropies=H[a:b].copy(), norms=N[a:b].copy()))
     return out
 
