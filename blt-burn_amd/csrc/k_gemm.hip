@@ -20,8 +20,10 @@ int device_cus() {
 template <int BM, int BN, int BK, int WM, int WN, int EPI>
 int run_gemm_persistent(const GemmArgs& a, hipStream_t s) {
   const int64_t nb = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-  // one block per CU, a multiple of 8 blocks so each keeps its XCD residue
-  int64_t grid = device_cus();
+  // as many blocks as fit on the CUs at once (256x256: one per CU, its LDS
+  // holds 160 KB; 128x128: two, 80 KB each), a multiple of 8 blocks so each
+  // keeps its XCD residue
+  int64_t grid = (int64_t)device_cus() * (BM * BN <= 128 * 128 ? 2 : 1);
   grid = grid >= 8 ? grid & ~7 : grid;
   if (grid <= 0 || grid > nb) grid = nb;
   hipLaunchKernelGGL((gemm::gemm_bf16_dma_persistent_kernel<BM, BN, BK, WM, WN, EPI>),
