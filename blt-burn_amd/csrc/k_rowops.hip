@@ -710,13 +710,46 @@ __global__ __launch_bounds__(PB_THREADS) void patch_boundary_kernel(
 constexpr int PM_THREADS = 256;
 constexpr int PM_TILE = 2048;
 
+// One chain's sums over LDS positions [a, z), left to right: the reads go 16
+// bytes at a time and run ahead of the dependent adds (unrolled body), the
+// order of the adds is the element order.
+template <bool HAS_C>
+__device__ inline void pm_chain(const float* sH, const float* sN, const float* sC, int a, int z,
+                                float& sh, float& sn, float& sc) {
+  int t = a;
+  for (; t < z && (t & 3); ++t) {
+    sh += sH[t];
+    sn += sN[t];
+    if (HAS_C) sc += sC[t];
+  }
+#pragma unroll 4
+  for (; t + 4 <= z; t += 4) {
+    const float4 h = *reinterpret_cast<const float4*>(sH + t);
+    const float4 q = *reinterpret_cast<const float4*>(sN + t);
+    sh += h.x; sh += h.y; sh += h.z; sh += h.w;
+    sn += q.x; sn += q.y; sn += q.z; sn += q.w;
+    if (HAS_C) {
+      const float4 c = *reinterpret_cast<const float4*>(sC + t);
+      sc += c.x; sc += c.y; sc += c.z; sc += c.w;
+    }
+  }
+  for (; t < z; ++t) {
+    sh += sH[t];
+    sn += sN[t];
+    if (HAS_C) sc += sC[t];
+  }
+}
+
+template <bool HAS_C>
 __global__ __launch_bounds__(PM_THREADS) void patch_means_kernel(
     const float* __restrict__ H, const float* __restrict__ N, const float* __restrict__ C,
     const int32_t* __restrict__ starts, const int32_t* __restrict__ count, int64_t T_dense,
     const int64_t* __restrict__ row_off, const int32_t* __restrict__ row_len,
     float* __restrict__ mH, float* __restrict__ mN, float* __restrict__ mC,
     const int64_t* __restrict__ out_off) {
-  __shared__ float sH[PM_TILE], sN[PM_TILE], sC[PM_TILE];
+  __shared__ __attribute__((aligned(16))) float sH[PM_TILE];
+  __shared__ __attribute__((aligned(16))) float sN[PM_TILE];
+  __shared__ __attribute__((aligned(16))) float sC[HAS_C ? PM_TILE : 4];
   __shared__ float carry[2][3];  // partial sums handed to the next tile
   __shared__ int32_t last[2];    // last patch started in the tile (atomicMax)
   const int64_t b = blockIdx.x;
@@ -751,7 +784,7 @@ __global__ __launch_bounds__(PM_THREADS) void patch_means_kernel(
     for (int i = tid; i < w; i += PM_THREADS) {
       sH[i] = H[roff + t0 + i];
       sN[i] = N[roff + t0 + i];
-      if (C) sC[i] = C[roff + t0 + i];
+      if (HAS_C) sC[i] = C[roff + t0 + i];
     }
     __syncthreads();
     // the next tile's counter, free since that tile's last read two syncs ago
@@ -775,12 +808,7 @@ __global__ __launch_bounds__(PM_THREADS) void patch_means_kernel(
       }
       const int a = (int)((st > t0 ? st : t0) - t0);
       const int z = (int)((e < t1 ? e : t1) - t0);
-#pragma unroll 8
-      for (int t = a; t < z; ++t) {
-        sh += sH[t];
-        sn += sN[t];
-        if (C) sc += sC[t];
-      }
+      pm_chain<HAS_C>(sH, sN, sC, a, z, sh, sn, sc);
       if (e <= t1) {
         put(p, sh, sn, sc, e - st);
       } else {  // only the tile's last chain runs on
@@ -1170,8 +1198,12 @@ int launch_patch_means(const float* H, const float* N, const float* C, const int
                        const int32_t* row_len, float* mH, float* mN, float* mC, hipStream_t s,
                        const int64_t* out_off) {
   if (B == 0) return 0;
-  hipLaunchKernelGGL(patch_means_kernel, dim3((unsigned)B), dim3(PM_THREADS), 0, s, H, N, C, starts,
-                     count, T, row_off, row_len, mH, mN, mC, out_off);
+  if (C)
+    hipLaunchKernelGGL(patch_means_kernel<true>, dim3((unsigned)B), dim3(PM_THREADS), 0, s, H, N,
+                       C, starts, count, T, row_off, row_len, mH, mN, mC, out_off);
+  else
+    hipLaunchKernelGGL(patch_means_kernel<false>, dim3((unsigned)B), dim3(PM_THREADS), 0, s, H, N,
+                       C, starts, count, T, row_off, row_len, mH, mN, mC, out_off);
   BLT_LAUNCH_CHECK("patch_means_kernel");
   return 0;
 }
