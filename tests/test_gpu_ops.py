@@ -529,6 +529,35 @@ def test_gemm_f32_epilogue_partial_columns(M, N):
     assert (c - ref).abs().max().item() <= 2e-3 * ref.abs().max().item()
 
 
+@pytest.mark.parametrize("epi", ["bf16", "resid", "f32", "silu", "qkv"])
+def test_gemm_small_launch_tiles_bit_identical(epi):
+    # A launch with fewer 256 x 256 tiles than CUs runs on 128 x 128 tiles; its
+    # rows must equal the same rows of a launch that stays on 256 x 256 tiles,
+    # bit for bit (the model's row-independence rests on it).
+    K, Mb, Ms = 768, 256 * 256 + 64, 1000
+    N = {"silu": 4096, "qkv": 2304}.get(epi, 768)
+    torch.manual_seed(5)
+    a = torch.randn(Mb, K, device=DEV).to(torch.bfloat16)
+    bt = (0.05 * torch.randn(N, K, device=DEV)).to(torch.bfloat16)
+    kw = {}
+    if epi == "qkv":
+        T = 512
+        kw = dict(rope_cols=1536, seq_len=T,
+                  cs=torch.from_numpy(oracle.rope_table(64, T, 10000.0)).to(DEV))
+    if epi == "f32":
+        kw = dict(n_valid=N)
+    code = {"bf16": _lib.EPI_BF16, "resid": _lib.EPI_RESID_F32, "f32": _lib.EPI_F32,
+            "silu": _lib.EPI_SILU_GATE, "qkv": _lib.EPI_QKV_ROPE}[epi]
+    if epi in ("resid", "f32"):
+        big = torch.randn(Mb, N, device=DEV)
+    else:
+        big = torch.zeros(Mb, N // 2 if epi == "silu" else N, device=DEV, dtype=torch.bfloat16)
+    small = big[:Ms].clone()
+    _gemm_epi(a, bt, big, code, **kw)
+    _gemm_epi(a[:Ms].contiguous(), bt, small, code, **kw)
+    assert torch.equal(small, big[:Ms])
+
+
 # ---------------------------------------------------------------- measurement probes
 def test_probe_copy_and_mfma():
     L = _lib.lib()
