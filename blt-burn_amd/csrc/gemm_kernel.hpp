@@ -744,18 +744,24 @@ void gemm_bf16_dma_persistent_kernel(GemmArgs p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
     for (int kt = 0; kt < KT; ++kt) {
-      // stage st ^ 1 was freed by the barrier that ended K tile kt - 1
-      if (kt + 1 < KT) {
-        dma_tile(kt + 1, st ^ 1);
-      } else if (more) {
-        tile_origin<BM, BN>(p, vn, m0n, n0n);
-        int ln = lane;
-        asm volatile("" : "+v"(ln));
-        set_tile(m0n, n0n, ln);
-        dma_tile(0, st ^ 1);
+      // stage st ^ 1 was freed by the barrier that ended K tile kt - 1: it takes
+      // K tile kt + 1, or after the last one the next tile's first (one DMA
+      // issue site for both keeps the loop body to one block)
+      bool dma_next = true;
+      int kt_next = kt + 1;
+      if (kt + 1 == KT) {
+        kt_next = 0;
+        dma_next = more;
+        if (more) {
+          tile_origin<BM, BN>(p, vn, m0n, n0n);
+          int ln = lane;
+          asm volatile("" : "+v"(ln));
+          set_tile(m0n, n0n, ln);
+        }
       }
       if (EPI == EPI_QKV_ROPE && kt + 1 == KT && n0 + wn * C::WTN < p.rope_cols)
         load_rope_cs(p, m0 + wm * C::WTM + lrow, lane, cs0);
+      if (dma_next) dma_tile(kt_next, st ^ 1);
       compute(st);
       if (kt + 1 < KT) dma_wait_barrier<0>();
       st ^= 1;
