@@ -135,3 +135,21 @@ def test_pipeline_closed_form_any_chunking():
         got = [(s, s + n) for s, n, *_ in r["patches"]]
         assert got == _closed_form_general(H, 1.0, C, S), (C, S, L)
         np.testing.assert_array_equal(r["entropies"], H)
+
+
+def test_patch_data_embedding_is_per_patch():
+    # pipeline.rs:46-60: every PatchData carries its own 768-float zero
+    # embedding; the mirror allocates it on first access
+    from blt_burn_amd.pipeline import EMBEDDING_DIM, PatchData
+    a = PatchData(3, 4, None, 1.5, 2.5, b"abcd")
+    b = PatchData(3, 4, None, 1.5, 2.5, b"abcd")
+    assert a.embedding.shape == (EMBEDDING_DIM,) and a.embedding.dtype == np.float32
+    assert not a.embedding.any()
+    assert a == b
+    a.embedding[0] = 1.0  # a patch's embedding is its own array
+    assert not b.embedding.any() and a != b
+    b.embedding = np.ones(EMBEDDING_DIM, np.float32)
+    assert b.embedding.sum() == EMBEDDING_DIM
+    c = PatchData(start_offset=0, length=1, prominence=0.5, entropy=0.25, bytes=b"x")
+    assert (c.start_offset, c.length, c.prominence, c.entropy, c.bytes) == (0, 1, 0.5, 0.25, b"x")
+    assert "start_offset=0" in repr(c)
