@@ -608,9 +608,13 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
       const uint16_t* sp = buf + r * LD + c * 8;
       const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(sp);
       const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(sp + 4);
+      // non-temporal: the tile's output is not read again by this launch, and
+      // the next kernel's reads of it (the whole output exceeds the MALL) come
+      // from HBM either way; every CU stores its slab at the same time here
       if (row < p.M)
-        *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(p.C) + row * p.ldc + ocol0 +
-                                    c * 8) = u32x4_t{lo.x, lo.y, hi.x, hi.y};
+        __builtin_nontemporal_store(u32x4_t{lo.x, lo.y, hi.x, hi.y},
+                                    reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(p.C) +
+                                                               row * p.ldc + ocol0 + c * 8));
     }
     wave_lds_fence();
   }
