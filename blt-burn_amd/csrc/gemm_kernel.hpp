@@ -5,10 +5,11 @@
 // projection, SiLU*gate of the fused W1|W3 FFN).
 //
 // Two kernels share the tiling and the epilogue layout:
-// gemm_bf16_dma_persistent_kernel (global -> LDS by DMA, 256 x 256 x 64 tiles,
-// one persistent block per CU, LDS-staged epilogue; every projection of the
-// model, N % 256 == 0) and gemm_bf16_kernel (register-staged loads; any N,
-// e.g. the 260-wide head).
+// gemm_bf16_dma_persistent_kernel (global -> LDS by DMA, 256 x 256 x 64 tiles
+// with one persistent block per CU, or 128 x 128 x 64 tiles with two for
+// launches that have fewer 256 x 256 tiles than CUs; LDS-staged epilogue; every
+// projection of the model, N % 256 == 0) and gemm_bf16_kernel (register-staged
+// loads; any N, e.g. the 260-wide head).
 //
 // Tiling: a BM x BN block tile is split over WM x WN wave64s; each wave owns a
 // (BM/WM) x (BN/WN) tile made of 32x32 v_mfma_f32_32x32x16_bf16 sub-tiles,
@@ -623,8 +624,9 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
 
 // Same tiling and epilogues as gemm_bf16_kernel, but K tiles move global ->
 // LDS by the LDS-DMA path (no VGPR staging, no ds_write) through two LDS
-// stages, and the kernel is persistent: one block per CU walks the tiles
-// v = blockIdx.x, blockIdx.x + gridDim.x, ...  With gridDim.x a multiple of 8
+// stages, and the kernel is persistent: each resident block (one per CU on
+// 256 x 256 tiles, two on 128 x 128) walks the tiles v = blockIdx.x,
+// blockIdx.x + gridDim.x, ...  With gridDim.x a multiple of 8
 // every tile of a block has the block's XCD residue, so the tile order of
 // tile_origin holds.  The K-tile stream runs on across tiles: the next tile's
 // first K tile is issued together with the current tile's last one, so its
