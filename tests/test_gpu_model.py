@@ -103,6 +103,16 @@ def _far_norm_weights(cfg, seed, hidden):
     return w
 
 
+@pytest.mark.parametrize("B,T", [(1, 1), (1, 2), (3, 3), (2, 33)])
+def test_entropy_model_few_tokens(B, T):
+    # a handful of tokens at real size: every projection runs on 128 x 128
+    # tiles that are almost all padding rows, attention on one partial key
+    # tile, the boundary pass on its T <= 2 special cases
+    cfg = M.entropy_model_config()
+    out, ref = _run(cfg, 2048, B, T, 512, seed=6)
+    _compare(out, ref, "entropy-model B=%d T=%d" % (B, T))
+
+
 @pytest.mark.parametrize("window,T", [(0, 256), (512, 700)])
 def test_entropy_model_far_norm_weights(window, T):
     # The RMSNorm weight scales the bf16 GEMM operand (bf16(x * w)); with
