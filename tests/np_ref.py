@@ -114,3 +114,56 @@ def model_forward(cfg, w, tokens):
     H = entropy(logits)
     return {"logits": logits, "pre_norm_embeddings": pre, "embedding_norms": norms,
             "entropies": H, "coherence_scores": norms ** 2 / (H + 1e-6)}
+
+
+def bf16_round(x):
+    """float32 values rounded to the nearest bfloat16 (ties to even)."""
+    x = np.ascontiguousarray(x, np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+def model_forward_bf16_operands(cfg, w, tokens, rounding=True):
+    """model_forward in float32 with the GEMM and attention operands rounded to
+    bf16 where a bf16-MFMA forward must round them: the RMSNorm-weighted
+    activations x * w (the 1 / rms row factor applied to the GEMM output), q
+    (scaled by 1 / sqrt(d) after RoPE), k and v, the softmax numerators P, the
+    attention output, the SiLU-gate product and the final norm's output.  With
+    rounding=False it is the float32 statement of the reference's math."""
+    D, L, Hn = cfg["dim"], cfg["n_layers"], cfg["n_heads"]
+    hd = D // Hn
+    eps, theta, window = cfg["norm_eps"], cfg["rope_theta"], cfg.get("window", 0)
+    r = bf16_round if rounding else (lambda t: np.asarray(t, np.float32))
+    W = {k: np.asarray(v, np.float32) for k, v in w.items()}
+    tokens = np.asarray(tokens)
+    B, T = tokens.shape
+    ang = rope_angles(hd, T, theta).astype(np.float32)
+    c, s = np.cos(ang), np.sin(ang)
+
+    def rot(t):
+        t1, t2 = t[..., : hd // 2], t[..., hd // 2:]
+        return np.concatenate([t1 * c - t2 * s, t1 * s + t2 * c], -1)
+
+    def heads(t):
+        return t.reshape(B, T, Hn, hd).transpose(0, 2, 1, 3)
+
+    def rstd(x):
+        return 1.0 / (np.sqrt((x * x).mean(-1, keepdims=True)) + eps)
+
+    mask = mask_matrix(T, True, window).astype(np.float32)
+    x = W["emb"][tokens]
+    for l in range(L):
+        a, f = r(x * W["attn_norm"][l]), rstd(x)
+        q = r(rot(heads((a @ W["wq"][l]) * f)) / np.float32(np.sqrt(hd)))
+        k = r(rot(heads((a @ W["wk"][l]) * f)))
+        v = r(heads((a @ W["wv"][l]) * f))
+        sc = q @ np.swapaxes(k, -1, -2) + mask
+        p = r(np.exp(sc - sc.max(-1, keepdims=True)))
+        o = (p @ v) / p.sum(-1, keepdims=True)
+        x = x + r(o.transpose(0, 2, 1, 3).reshape(B, T, D)) @ W["wo"][l]
+        a, f = r(x * W["ffn_norm"][l]), rstd(x)
+        g, u = (a @ W["w1"][l]) * f, (a @ W["w3"][l]) * f
+        x = x + r(g / (1 + np.exp(-g)) * u) @ W["w2"][l]
+    logits = r(x * rstd(x) * W["norm"]) @ W["out"]
+    return {"logits": logits, "pre_norm_embeddings": x, "entropies": entropy(logits)}

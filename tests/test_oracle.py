@@ -190,3 +190,27 @@ def test_model_forward_vs_float64(window):
     ref = np_ref.model_forward(cfg, w, tok)
     for k in ("logits", "pre_norm_embeddings", "embedding_norms", "entropies", "coherence_scores"):
         np.testing.assert_allclose(got[k], ref[k], rtol=1e-4, atol=1e-4, err_msg=k)
+
+
+def test_bf16_round_and_operand_emulation():
+    # bf16 rounding: nearest, ties to even, low 16 bits cleared
+    x = np.array([1.0, 1.00390625, 1.005859375, 1.01171875, -3.14159, 65504.0], np.float32)
+    np.testing.assert_array_equal(np_ref.bf16_round(x),
+                                  np.array([1.0, 1.0, 1.0078125, 1.015625, -3.140625, 65536.0],
+                                           np.float32))
+    y = np.random.default_rng(3).normal(0, 10, 4096).astype(np.float32)
+    r = np_ref.bf16_round(y)
+    assert not (r.view(np.uint32) & 0xFFFF).any()
+    assert (np.abs(r - y) <= np.abs(y) * 2.0 ** -8).all()  # half of an 8-bit significand step
+    # the float32 forward with rounding off is the reference's math (the C oracle)
+    cfg, w = _tiny_model()
+    cfg["window"] = 8
+    tok = np.random.default_rng(9).integers(0, 260, (2, 33)).astype(np.int32)
+    ref = oracle.model_forward(cfg, w, tok)
+    ex = np_ref.model_forward_bf16_operands(cfg, w, tok, rounding=False)
+    for k in ("logits", "pre_norm_embeddings", "entropies"):
+        np.testing.assert_allclose(ex[k], ref[k], rtol=1e-4, atol=1e-4, err_msg=k)
+    # with rounding on it moves, by about the bf16 step and not more
+    em = np_ref.model_forward_bf16_operands(cfg, w, tok)
+    d = np.abs(em["logits"] - ref["logits"]).max() / np.abs(ref["logits"]).max()
+    assert 1e-4 < d < 2e-2, d
