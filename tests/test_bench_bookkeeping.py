@@ -1,0 +1,89 @@
+"""The bench's profiler bookkeeping, on synthetic rocprofv3 CSVs: dispatches of
+one forward mapped to model stages, and the per-stage HBM traffic per launch
+(counter values scaled by what the same counter reads for a copy of known
+size), which the bench line's roofline.traffic reports.  CPU only."""
+import argparse
+import csv
+import importlib.util
+import os
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+_spec = importlib.util.spec_from_file_location("bench_mod", os.path.join(ROOT, "bench.py"))
+bench = importlib.util.module_from_spec(_spec)
+_spec.loader.exec_module(bench)
+
+L = 14
+G = "void blt::gemm::gemm_bf16_dma_persistent_kernel<256, 256, 64, 2, 4, %d>(blt::GemmArgs)"
+
+
+def _forward_names(layers):
+    n = ["blt::embed_kernel(int const*)"]
+    for _ in range(layers):
+        n += [G % 3, "void blt::(anonymous namespace)::attn_fwd_kernel<1>(blt::AttnArgs)",
+              G % 2, "blt::row_rstd_kernel(float const*)", G % 4, G % 2,
+              "blt::row_rstd_kernel(float const*)"]
+    n += ["void blt::rmsnorm_kernel<float, float, unsigned short, 4, 3>(float const*)",
+          "void blt::gemm::gemm_bf16_kernel<128, 128, 32, 2, 2, 2, 3>(blt::GemmArgs)",
+          "void blt::entropy_half_kernel<float, 2, 1>(float const*)",
+          "blt::coherence_kernel(float const*)",
+          "blt::(anonymous namespace)::patch_flags_kernel(blt::PatchKArgs)",
+          "blt::(anonymous namespace)::patch_compact_kernel(blt::PatchKArgs)"]
+    return n
+
+
+def test_dispatch_stages_one_forward():
+    st = bench._dispatch_stages(_forward_names(2), 2)
+    assert st[0] == "embed"
+    layer = ["qkv_gemm_rope", "attention", "o_gemm_residual", None, "w13_gemm_silu",
+             "w2_gemm_residual", None]
+    assert st[1:15] == layer * 2
+    assert st[15:] == ["rmsnorm", "head_gemm", "entropy", "coherence", "patch_boundaries",
+                       "patch_boundaries"]
+    assert bench._dispatch_stages(["blt::(anonymous namespace)::mfma_peak_kernel(int, float*)",
+                                   "at::native::copy"], 2) == [None, None]
+
+
+def _write_counters(d, counter, rows):
+    os.makedirs(os.path.join(d, "host"), exist_ok=True)
+    with open(os.path.join(d, "host", "p_counter_collection.csv"), "w", newline="") as f:
+        w = csv.DictWriter(f, ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+        w.writeheader()
+        for i, (name, v) in enumerate(rows):
+            w.writerow({"Dispatch_Id": i + 1, "Kernel_Name": name, "Counter_Name": counter,
+                        "Counter_Value": v})
+
+
+def test_summarize_scales_and_averages(tmp_path, capsys):
+    names = _forward_names(L)
+    # a peak probe before the forward (not a stage), then one forward; the
+    # W1|W3 launches read 1000 + layer KiB and write 500 KiB each
+    pre = [("blt::(anonymous namespace)::mfma_peak_kernel(int, float*)", 7.0)]
+    fetch, write, layer = list(pre), list(pre), 0
+    for n in names:
+        f, wv = 10.0, 20.0
+        if n == G % 4:
+            f, wv = 1000.0 + layer, 500.0
+            layer += 1
+        fetch.append((n, f))
+        write.append((n, wv))
+    copy = 1 << 20  # bytes the copy probe moves
+    _write_counters(str(tmp_path / "tf"), "FETCH_SIZE", fetch)
+    _write_counters(str(tmp_path / "tw"), "WRITE_SIZE", write)
+    # the copy reads half its bytes on FETCH_SIZE and all of them on WRITE_SIZE
+    _write_counters(str(tmp_path / "cf"), "FETCH_SIZE", [("copy", copy / 2048.0)])
+    _write_counters(str(tmp_path / "cw"), "WRITE_SIZE", [("copy", copy / 1024.0)])
+    args = argparse.Namespace(summarize=[str(tmp_path / x) for x in ("tf", "tw", "cf", "cw")],
+                              copy_bytes=float(copy))
+    bench.summarize(args)
+    import json
+    res = json.loads(capsys.readouterr().out)
+    assert res["fetch_scale"] == pytest.approx(2.0) and res["write_scale"] == pytest.approx(1.0)
+    w13 = res["stages"]["w13_gemm_silu"]
+    assert w13["launches"] == L
+    assert w13["fetch_bytes"] == round((1000.0 + (L - 1) / 2.0) * 1024 * 2.0)
+    assert w13["write_bytes"] == 500 * 1024
+    assert res["stages"]["head_gemm"]["launches"] == 1
+    assert res["stages"]["qkv_gemm_rope"]["fetch_bytes"] == 10 * 1024 * 2
+    assert "mfma_peak" not in json.dumps(res["stages"])
