@@ -87,3 +87,33 @@ def test_summarize_scales_and_averages(tmp_path, capsys):
     assert res["stages"]["head_gemm"]["launches"] == 1
     assert res["stages"]["qkv_gemm_rope"]["fetch_bytes"] == 10 * 1024 * 2
     assert "mfma_peak" not in json.dumps(res["stages"])
+
+
+def test_summarize_trace_means_per_stage(tmp_path, capsys):
+    # a probe before the first forward, then two forwards: W1|W3 launches take
+    # 700 us in the first and 800 us in the second, every other kernel 10 us
+    rows, t, did = [], 0, 0
+    seq = [("blt::(anonymous namespace)::mfma_peak_kernel(int, float*)", 0)]
+    for fwd in range(2):
+        seq += [(n, fwd) for n in _forward_names(L)]
+    for n, fwd in seq:
+        dur = (700 + 100 * fwd) * 1000 if n == G % 4 else 10 * 1000
+        did += 1
+        rows.append({"Dispatch_Id": did, "Kernel_Name": n, "Start_Timestamp": t,
+                     "End_Timestamp": t + dur})
+        t += dur + 5000
+    p = tmp_path / "trace.csv"
+    with open(p, "w", newline="") as f:
+        w = csv.DictWriter(f, ["Dispatch_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        w.writerows(rows[::-1])  # the summary sorts by dispatch id itself
+    bench.summarize_trace(str(p))
+    lines = capsys.readouterr().out.splitlines()
+    table = {c[1].strip(): c for c in (ln.split("|") for ln in lines[2:])}
+    w13 = table["w13_gemm_silu"]
+    assert w13[2].strip() == "`" + (G % 4)[:(G % 4).rfind("(")] + "`"
+    assert (int(w13[3]), float(w13[4]), float(w13[5])) == (2 * L, 750.0, 2 * L * 750.0)
+    assert lines[2].split("|")[1].strip() == "w13_gemm_silu"  # largest total first
+    assert (int(table["head_gemm"][3]), float(table["head_gemm"][4])) == (2, 10.0)
+    assert int(table["o_gemm_residual"][3]) == 2 * L
+    assert "mfma_peak" not in "".join(lines)
