@@ -44,6 +44,7 @@ EXPORTS = {
     "blt_rope_table_f32": (c_i32, [c_vp, c_i32, c_i32, c_f64, c_vp]),
     "blt_patch_boundaries": (c_i32, [c_vp, c_i64, c_i64, c_f32, c_i32, c_vp, c_vp, c_vp, c_vp,
                                      c_vp]),
+    "blt_patch_mask_starts": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp]),
     "blt_patch_means": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp,
                                 c_vp]),
     "blt_patch_workspace_bytes": (c_i64, [c_i64, c_i64, c_i32]),
@@ -56,6 +57,7 @@ EXPORTS = {
     "blt_model_device_bytes": (c_i64, [c_vp]),
     "blt_model_forward": (c_i32, [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp]),
     "blt_model_forward_segments": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp]),
+    "blt_model_extract_embeddings": (c_i32, [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp]),
     "blt_tokenize_bytes": (c_i32, [c_vp, c_i64, c_i32, c_i32, c_vp, c_i64, c_vp]),
     "blt_tokenize_documents": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_i64, c_vp]),
     "blt_ingest_plan_chunks": (c_i32, [c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i64]),

@@ -321,6 +321,17 @@ int blt_patch_boundaries(const float* H, int64_t B, int64_t T, float thr, int32_
                                  STREAM(stream));
 }
 
+int blt_patch_mask_starts(const int32_t* mask, int64_t B, int64_t T, int32_t* starts,
+                          int32_t* lengths, int32_t* count, blt_stream_t stream) {
+  if (B < 0 || T < 0) return fail(BLT_ERR_SHAPE, "patch_mask_starts: negative shape");
+  if (T > 0x7fffffff) return fail(BLT_ERR_SHAPE, "patch_mask_starts: T must fit int32");
+  if (lengths && !starts)
+    return fail(BLT_ERR_INVALID, "patch_mask_starts: lengths needs the starts buffer");
+  if (B == 0) return BLT_OK;
+  if (T > 0 && !mask) return fail(BLT_ERR_INVALID, "patch_mask_starts: null mask");
+  return launch_patch_mask_starts(mask, B, T, starts, lengths, count, STREAM(stream));
+}
+
 int blt_patch_means(const float* entropies, const float* norms, const float* coherence,
                     const int32_t* starts, const int32_t* count, int64_t B, int64_t T,
                     float* mean_entropy, float* mean_prominence, float* mean_coherence,
@@ -379,6 +390,15 @@ int blt_model_forward(blt_model* m, const int32_t* tokens, int64_t B, int64_t T,
                       const blt_model_outputs* out, blt_stream_t stream) {
   if (!m || !out) return fail(BLT_ERR_INVALID, "model_forward: null argument");
   return reinterpret_cast<Model*>(m)->forward(tokens, B, T, *out, STREAM(stream));
+}
+
+int blt_model_extract_embeddings(blt_model* m, const int32_t* tokens, int64_t B, int64_t T,
+                                 float* out, blt_stream_t stream) {
+  if (!m) return fail(BLT_ERR_INVALID, "model_extract_embeddings: null model");
+  if (!out && B * T > 0) return fail(BLT_ERR_INVALID, "model_extract_embeddings: null output");
+  blt_model_outputs o{};
+  o.pre_norm_embeddings = out;
+  return reinterpret_cast<Model*>(m)->forward(tokens, B, T, o, STREAM(stream));
 }
 
 int blt_model_forward_segments(blt_model* m, const int32_t* tokens, const int32_t* seg_start,

@@ -574,6 +574,10 @@ __global__ __launch_bounds__(256) void rope64_kernel(const uint16_t* __restrict_
 // ---------------------------------------------------------------------------
 #define PB_THREADS 1024
 #define PB_ITEMS 8  // the vector path below loads and stores them as two 16-byte pieces
+// mode of patch_boundary_kernel whose input is a start mask (int32 bits read
+// through the f32 pointer): flag[t] = (mask[t] == 1) at every t, the test of
+// patch_start_indices_cpu (patcher.rs:131-136)
+#define PB_MODE_MASK 2
 
 // Row b covers H[off_b, off_b + T_b): off_b = b * T and T_b = T for a dense
 // [B, T] input, or row_off[b] / row_len[b] for variable-length rows (the
@@ -627,7 +631,8 @@ __global__ __launch_bounds__(PB_THREADS) void patch_boundary_kernel(
       const int64_t t = p0 + k;
       int f = 0;
       if (t < T) {
-        if (t < 2) f = 1;
+        if (mode == PB_MODE_MASK) f = __builtin_bit_cast(int32_t, cur[k]) == 1;
+        else if (t < 2) f = 1;
         else if (mode == 0) f = (cur[k] - prev) > thr;
         else f = cur[k] > thr;
         prev = cur[k];
@@ -1123,6 +1128,16 @@ int launch_patch_boundaries(const float* H, int64_t B, int64_t T, float thr, int
   if (B == 0) return 0;
   hipLaunchKernelGGL(patch_boundary_kernel, dim3((unsigned)B), dim3(PB_THREADS), 0, s, H, T, thr,
                      mode, mask, starts, lengths, count, nullptr, nullptr);
+  BLT_LAUNCH_CHECK("patch_boundary_kernel");
+  return 0;
+}
+
+int launch_patch_mask_starts(const int32_t* mask, int64_t B, int64_t T, int32_t* starts,
+                             int32_t* lengths, int32_t* count, hipStream_t s) {
+  if (B == 0) return 0;
+  hipLaunchKernelGGL(patch_boundary_kernel, dim3((unsigned)B), dim3(PB_THREADS), 0, s,
+                     reinterpret_cast<const float*>(mask), T, 0.f, PB_MODE_MASK, nullptr, starts,
+                     lengths, count, nullptr, nullptr);
   BLT_LAUNCH_CHECK("patch_boundary_kernel");
   return 0;
 }

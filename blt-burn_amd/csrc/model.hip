@@ -319,8 +319,23 @@ int Model::forward(const int32_t* tokens, int64_t B, int64_t T, const blt_model_
     if (next && (rc = launch_row_rstd(ss, rstd, M, np, (int)D, cfg.norm_eps, s))) return rc;
     if ((rc = mark(BLT_STAGE_W2_GEMM, s))) return rc;
   }
-  // pre-norm L2 norms fused with the final RMSNorm (one read of the residual)
+  // Only what the caller asked for: the head (final norm, logits, entropy)
+  // runs when logits, entropies or coherence are wanted; the norms alone are
+  // one read of the residual; the residual alone (extract_embeddings,
+  // model.rs:325-345) stops here.
+  const bool need_head = o.logits || o.entropies || o.coherence_scores;
+  const bool need_norms = o.embedding_norms || o.coherence_scores;
   float* nr = o.embedding_norms ? o.embedding_norms : norms;
+  if (!need_head) {
+    if (need_norms) {
+      if ((rc = launch_rmsnorm<float, float, float>(xr, nullptr, nullptr, nr, M, (int)D, 0.f, 0,
+                                                    s)))
+        return rc;
+      if ((rc = mark(BLT_STAGE_FINAL_NORM, s))) return rc;
+    }
+    return 0;
+  }
+  // pre-norm L2 norms fused with the final RMSNorm (one read of the residual)
   if ((rc = launch_rmsnorm<float, float, uint16_t>(xr, final_norm, a, nr, M, (int)D, cfg.norm_eps,
                                                    0, s)))
     return rc;

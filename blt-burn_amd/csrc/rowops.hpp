@@ -32,6 +32,9 @@ int launch_rope(const uint16_t* src, uint16_t* dst, const float* cs, int64_t B, 
 int launch_patch_boundaries(const float* H, int64_t B, int64_t T, float thr, int mode,
                             int32_t* mask, int32_t* starts, int32_t* lengths, int32_t* count,
                             hipStream_t s);
+// the same compaction from a start mask: starts = {t : mask[b, t] == 1}
+int launch_patch_mask_starts(const int32_t* mask, int64_t B, int64_t T, int32_t* starts,
+                             int32_t* lengths, int32_t* count, hipStream_t s);
 
 // per-patch means of H / N / C over the patches starts[0 .. count) of each row
 // (row_off / row_len NULL: dense rows of T); C, mH, mN, mC may be NULL.

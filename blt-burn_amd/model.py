@@ -126,6 +126,9 @@ class LMTransformer:
                    hidden=shp["hidden"])
 
     def __del__(self):
+        # pipeline buffers cached on this model hold handles into it: free them first
+        for buf in self.__dict__.pop("_pipeline_cache", {}).values():
+            buf.close()
         h = getattr(self, "_h", None)
         # at interpreter exit the module globals may already be gone
         if h is not None and h.value and _lib is not None and _lib._lib is not None:
@@ -176,6 +179,29 @@ class LMTransformer:
                 self._h, tok.data_ptr(), seg_start.data_ptr(), B, T, ctypes.byref(o),
                 stream_ptr(tok.device)), "blt_model_forward_segments")
         return ModelOutput(**res)
+
+    def extract_embeddings(self, tokens, out=None):
+        """LMTransformer::extract_embeddings (model.rs:325-345, 413-431): the
+        pre-normalisation residual after the last layer, f32 [B, T, D].  No
+        final norm, head, entropy or coherence is computed.  `out` may pass the
+        result tensor preallocated (contiguous f32 [B, T, D] on this GPU)."""
+        require_cuda(tokens)
+        if tokens.dim() != 2:
+            raise BltError("extract_embeddings expects tokens [batch, seq]")
+        tok = tokens if (tokens.dtype == torch.int32 and tokens.is_contiguous()) \
+            else tokens.to(torch.int32).contiguous()
+        B, T = tok.shape
+        shp = (B, T, self.cfg.dim)
+        if out is None:
+            out = torch.empty(shp, dtype=torch.float32, device=tok.device)
+        elif (tuple(out.shape) != shp or out.dtype != torch.float32 or not out.is_contiguous()
+              or out.device != tok.device):
+            raise BltError("extract_embeddings: out must be contiguous f32 %s on the tokens' "
+                           "device" % (shp,))
+        check(_lib.lib().blt_model_extract_embeddings(self._h, tok.data_ptr(), B, T,
+                                                      out.data_ptr(), stream_ptr(tok.device)),
+              "blt_model_extract_embeddings")
+        return out
 
     def set_profiling(self, on=True):
         """Record HIP events between the forward's kernels (per-stage timing)."""

@@ -2,15 +2,17 @@
 
 entropy / patch_start_mask_from_entropy_with_monotonicity keep the reference's
 signatures; the device pass behind them also compacts start indices and
-lengths (patch_boundaries), so patch_start_indices_cpu only copies results.
+lengths (patch_boundaries), and patch_start_indices_cpu compacts a mask on the
+device when it lives on a GPU, so only the results are copied to the host.
 
 The pass runs many blocks per row and passes per-tile counts and flag words
-between its kernels through a per-device workspace, so calls on one device
-must be stream-ordered: torch's current stream of one thread, or streams the
-caller orders.  Two rules (e.g. the global and the
-monotonic mask) can share one read of the entropies (patch_boundaries_rules),
-and entropy_patch_boundaries computes the entropies and the rules in one pass
-over the logits.
+between its kernels through a workspace.  Each call takes its own from torch's
+caching allocator on the current stream, so calls on different streams or
+threads never share one (the allocator hands a freed block out again only to
+later work on the same stream).  Two rules (e.g. the global and the monotonic
+mask) can share one read of the entropies (patch_boundaries_rules), and
+entropy_patch_boundaries computes the entropies and the rules in one pass over
+the logits.
 """
 import torch
 
@@ -21,7 +23,7 @@ from .fused_ops import fused_entropy
 
 __all__ = ["entropy", "patch_start_mask_from_entropy_with_monotonicity",
            "patch_start_mask_global", "patch_boundaries", "patch_boundaries_rules",
-           "entropy_patch_boundaries", "patch_start_indices_cpu",
+           "entropy_patch_boundaries", "patch_start_indices_cpu", "patch_mask_starts",
            "patch_lengths_from_start_indices", "patch_means", "PATCH_MONOTONIC",
            "PATCH_GLOBAL"]
 
@@ -31,23 +33,12 @@ def entropy(scores):
     return fused_entropy(scores, scores.shape[-1])
 
 
-_WORKSPACE = {}  # device index -> uint8 tensor passed between the pass's kernels
-
-
 def _workspace(device, nbytes):
-    """The device's boundary-pass workspace, grown when a call needs more;
-    growing it inside a HIP graph capture is refused (run the call once
-    eagerly first, as the capture then reuses it)."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    ws = _WORKSPACE.get(idx)
-    if ws is None or ws.numel() < nbytes:
-        if torch.cuda.is_current_stream_capturing():
-            raise BltError("the patch workspace must exist before graph capture: run the "
-                           "boundary pass once eagerly first")
-        ws = torch.empty(max(int(nbytes), 1 << 16), dtype=torch.uint8,
-                         device=torch.device("cuda", idx))
-        _WORKSPACE[idx] = ws
-    return ws
+    """A workspace for one boundary pass on `device`, allocated on the current
+    stream (where the pass runs): the caching allocator keeps this cheap, and
+    the block returns to that stream's pool when the call's tensor is dropped,
+    after the kernels queued on it."""
+    return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
 
 
 def _rule_outputs(B, T, device, out):
@@ -135,8 +126,9 @@ class EntropyPatchPlan:
     allocated, the rule array and the workspace bound, once; each call checks
     the logits and makes the one library call (the per-call checks of a dozen
     tensors cost the function form more host time than the device pass).
-    Calls return the same output tensors each time and must be stream-ordered
-    with any other boundary pass that shares the device's workspace."""
+    Calls return the same output tensors and reuse the plan's own workspace
+    each time, so the calls of one plan must be stream-ordered (one plan per
+    stream or thread); separate plans and the function forms share nothing."""
 
     def __init__(self, batch, seq, vocab, rules, device=None):
         dev = torch.device("cuda" if device is None else device)
@@ -190,11 +182,47 @@ def patch_start_mask_global(entropies, threshold):
 
 
 def patch_start_indices_cpu(patch_start_mask):
-    """Per-row lists of positions whose mask is 1 (patcher.rs:124-142)."""
-    m = patch_start_mask.detach().to("cpu")
-    if m.dim() != 2:
+    """Per-row lists of positions whose mask is exactly 1 (patcher.rs:124-142).
+
+    A mask on a GPU is compacted there (blt_patch_mask_starts) and only the
+    starts and counts come back; a host tensor is scanned on the host, which
+    is what the reference's function does with the data it reads back."""
+    if patch_start_mask.dim() != 2:
         raise BltError("patch_start_indices_cpu expects [batch, seq]")
-    return [torch.nonzero(row == 1).flatten().tolist() for row in m]
+    if not patch_start_mask.is_cuda:
+        m = patch_start_mask.detach()
+        return [torch.nonzero(row == 1).flatten().tolist() for row in m]
+    m = contiguous(patch_start_mask if patch_start_mask.dtype == torch.int32
+                   else patch_start_mask.to(torch.int32))
+    B, T = m.shape
+    starts = torch.empty((B, T), dtype=torch.int32, device=m.device)
+    counts = torch.empty((B,), dtype=torch.int32, device=m.device)
+    check(_lib.lib().blt_patch_mask_starts(m.data_ptr(), B, T, starts.data_ptr(), None,
+                                           counts.data_ptr(), stream_ptr(m.device)),
+          "patch_mask_starts")
+    ct = counts.cpu().tolist()
+    n = max(ct) if ct else 0
+    st = starts[:, :n].cpu().tolist()
+    return [st[b][:ct[b]] for b in range(B)]
+
+
+def patch_mask_starts(patch_start_mask):
+    """Device compaction of a start mask [batch, seq] (patcher.rs:124-164):
+    (starts [B, T], lengths [B, T], counts [B]) int32 on the mask's GPU, laid
+    out as patch_boundaries returns them."""
+    require_cuda(patch_start_mask)
+    if patch_start_mask.dim() != 2:
+        raise BltError("patch_mask_starts expects [batch, seq]")
+    m = contiguous(patch_start_mask if patch_start_mask.dtype == torch.int32
+                   else patch_start_mask.to(torch.int32))
+    B, T = m.shape
+    starts = torch.empty((B, T), dtype=torch.int32, device=m.device)
+    lengths = torch.empty((B, T), dtype=torch.int32, device=m.device)
+    counts = torch.empty((B,), dtype=torch.int32, device=m.device)
+    check(_lib.lib().blt_patch_mask_starts(m.data_ptr(), B, T, starts.data_ptr(),
+                                           lengths.data_ptr(), counts.data_ptr(),
+                                           stream_ptr(m.device)), "patch_mask_starts")
+    return starts, lengths, counts
 
 
 def patch_lengths_from_start_indices(start_indices, seq_len):

@@ -10,6 +10,7 @@ as packed segments of large forwards and each document's patches come out
 exactly as process_document's chunk loop emits them.
 """
 import ctypes
+import weakref
 from dataclasses import dataclass
 from typing import List
 
@@ -94,9 +95,19 @@ class PipelineBuffer:
     def __init__(self, threshold):
         self.threshold = float(threshold)
         self._h = None
-        self._model = None
+        self._strong = None  # the bound model (None when bound weakly)
+        self._wref = None
 
-    def _bind(self, model):
+    @property
+    def _model(self):
+        return self._wref() if self._wref is not None else None
+
+    def _bind(self, model, weak=False):
+        """Bind the model on first use.  A buffer the caller holds keeps its
+        model alive; the per-model buffers of process_document /
+        process_documents bind weakly (they live on the model, which closes
+        them before it frees itself), so no reference cycle holds the model's
+        device memory after the caller drops it."""
         if self._h is None:
             if model is None or not hasattr(model, "_h"):
                 raise BltError("PipelineBuffer.process_chunk needs the entropy model (an "
@@ -105,15 +116,20 @@ class PipelineBuffer:
             check(_lib.lib().blt_pipeline_create(model._h, self.threshold, ctypes.byref(h)),
                   "blt_pipeline_create")
             self._h = h
-            self._model = model
+            self._strong = None if weak else model
+            self._wref = weakref.ref(model)
         elif model is not None and model is not self._model:
             raise BltError("a PipelineBuffer runs one model; this one is bound to another")
 
-    def __del__(self):
+    def close(self):
+        """Free the device state (the accumulated signals and staging buffers)."""
         h = getattr(self, "_h", None)
         if h is not None and h.value and _lib is not None and _lib._lib is not None:
             _lib.lib().blt_pipeline_destroy(h)
-            self._h = None
+        self._h = None
+
+    def __del__(self):
+        self.close()
 
     def _stream(self):
         return stream_ptr(self._model.device)
@@ -243,7 +259,7 @@ def _buffer_for(model, threshold):
     buf = cache.get(key)
     if buf is None:
         buf = PipelineBuffer(threshold)
-        buf._bind(model)
+        buf._bind(model, weak=True)
         cache[key] = buf
     return buf
 

@@ -151,6 +151,17 @@ int blt_patch_boundaries(const float* H, int64_t B, int64_t T, float thr, int32_
                          int32_t* mask, int32_t* starts, int32_t* lengths, int32_t* count,
                          blt_stream_t stream);
 
+/* patch_start_indices_cpu (patcher.rs:124-142) and patch_lengths_from_start_indices
+ * (patcher.rs:144-164) on the device, from a start mask such as
+ * patch_start_mask_from_entropy_with_monotonicity returns: the starts of row b
+ * are the positions t with mask[b*T + t] == 1 (exactly 1, as the reference
+ * tests), ascending; lengths are next start (or T) minus start.
+ *   mask [B, T] int32.  Outputs as blt_patch_boundaries writes them: starts /
+ *   lengths [B, T] int32 with count[b] valid entries per row, count [B] int32
+ *   (each may be NULL; lengths needs starts). */
+int blt_patch_mask_starts(const int32_t* mask, int64_t B, int64_t T, int32_t* starts,
+                          int32_t* lengths, int32_t* count, blt_stream_t stream);
+
 /* One boundary rule and its outputs, laid out as blt_patch_boundaries writes
  * them (each output may be NULL; lengths needs starts). */
 typedef struct blt_patch_rule {
@@ -274,6 +285,14 @@ int64_t blt_model_device_bytes(const blt_model* m);
  * tokens [B, T] int32 device buffer; 1 <= T <= max_seqlen, B*T <= max_tokens. */
 int blt_model_forward(blt_model* m, const int32_t* tokens, int64_t B, int64_t T,
                       const blt_model_outputs* out, blt_stream_t stream);
+
+/* LMTransformer::extract_embeddings (model.rs:325-345, 413-431): the
+ * pre-normalisation residual after the last layer, out [B, T, dim] f32 (device,
+ * caller-owned).  It stops there: no final RMSNorm, head GEMM, entropy or
+ * coherence runs.  (blt_model_forward likewise skips the head when its
+ * logits, entropies and coherence_scores outputs are all NULL.) */
+int blt_model_extract_embeddings(blt_model* m, const int32_t* tokens, int64_t B, int64_t T,
+                                 float* out, blt_stream_t stream);
 
 /* Packed rows: several independent sequences (segments) per row, as the
  * reference would run them one by one (model.rs:269-322 per sequence; the

@@ -130,6 +130,14 @@ def test_tiny_model_far_norm_weights():
     _compare(out, ref, "tiny far-norm")
 
 
+# Absolute ceilings on the entropy deviation from the fp32 oracle with spread
+# entropies, just above what this build measures, so a precision regression
+# fails even where the emulation bar below would still pass.  They exceed the
+# 2e-2 bar of the N(0, 0.02) configurations: a known parity gap of bf16
+# matrix-core operands on trained-like weights.
+SPREAD_CEILING = {(0.1, 0.03): 5.5e-2, (0.12, 0.05): 0.24}
+
+
 @pytest.mark.parametrize("out_std,std", [(0.1, 0.03), (0.12, 0.05)])
 def test_entropy_model_spread_entropies(out_std, std):
     # With N(0, 0.02) weights every entropy sits near ln 260.  A larger output
@@ -169,6 +177,7 @@ def test_entropy_model_spread_entropies(out_std, std):
     assert Hr.min() < 2.0 and Hr.max() - Hr.min() > 1.5, (Hr.min(), Hr.max())
     for g, e in zip(dg, de):
         assert g <= 1.5 * e + 1e-3, (dg, de)
+    assert dg[0] < SPREAD_CEILING[(out_std, std)], dg
     n = out.embedding_norms.cpu().numpy()
     assert (np.abs(n - ref["embedding_norms"]) / ref["embedding_norms"]).max() < 1e-2
     # Boundaries from the GPU's entropies: bit-exact against the oracle's rule
