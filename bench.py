@@ -165,6 +165,14 @@ def main():
     ap.add_argument("--cpu-seq", type=int, default=4096,
                     help="tokens of the CPU-oracle sample (B=1)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--telemetry-s", type=float, default=2.0,
+                    help="config 4: seconds of extra steps after the timed ones with the "
+                         "GPU's power, PPT residency and clocks recorded (0 = off)")
+    ap.add_argument("--power-stages", action="store_true",
+                    help="each config-4 stage alone (its kernel on config-4 shapes, back to "
+                         "back for --stage-s seconds) with power, PPT residency and clocks; "
+                         "one JSON line")
+    ap.add_argument("--stage-s", type=float, default=1.5)
     ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles",
                                                            "traffic_config4.json"),
                     help="per-stage HBM bytes per launch measured with rocprofv3 --pmc")
@@ -212,6 +220,9 @@ def main():
         sys.exit(1)
     if args.pipeline:
         bench_pipeline(args)
+        return
+    if args.power_stages:
+        bench_power_stages(args)
         return
     if args.config == 5:
         bench_ingest(args)
@@ -296,6 +307,10 @@ def main():
         "stage_ms_per_step": stage_ms,
         "cpu_baseline": None,
     }
+    if args.telemetry_s > 0:
+        # after the timed steps, outside `value`: what the power manager did
+        # while the same step ran back to back
+        result["telemetry"] = telemetry_window(step, args.telemetry_s, sync_every=2)
 
     if not args.no_cpu:
         import oracle  # the checker / CPU baseline only
@@ -383,6 +398,208 @@ def _with_achievable(roof):
     roof["achievable_peak"] = ach
     roof["frac_of_achievable"] = round(roof["achieved"] / ach, 4)
     return roof
+
+
+def _amdsmi_handle():
+    """amdsmi's handle of the GPU the bench runs on, or None when the module or
+    the device's metrics table is not available."""
+    try:
+        import amdsmi
+        amdsmi.amdsmi_init()
+        hs = amdsmi.amdsmi_get_processor_handles()
+        if not hs:
+            return None
+        amdsmi.amdsmi_get_gpu_metrics_info(hs[0])
+        return hs[0]
+    except Exception:  # no telemetry on this system: the bench line omits it
+        return None
+
+
+def _metric(m, key):
+    v = m.get(key)
+    return v if isinstance(v, (int, float)) else None
+
+
+def telemetry_window(fn, seconds, sync_every=8):
+    """Runs fn() back to back for about `seconds` and reports what the GPU's
+    power manager saw meanwhile, from amdsmi's metrics table (the firmware
+    refreshes it every few tens of ms; every figure below is a delta of its
+    accumulators between the first and last table read inside the busy
+    window, timed by the table's own clock):
+      power_w        mean socket power: energy accumulator delta (times the
+                     counter resolution) over system_clock_counter delta
+      residency      fraction of the window each limiter was active
+                     (<name>_residency_acc delta / accumulation_counter delta):
+                     ppt = package power limit, prochot, socket_thm, vr_thm,
+                     hbm_thm = thermal limits
+      xcd_*          per XCD, fraction of the window its graphics clock was
+                     held below the host limit (total, by PPT, by thermal) or
+                     its utilisation was low, from xcp_stats
+      gfxclk_mhz     current graphics clock of the 8 XCDs, read every 20 ms by
+                     a host thread (mean, min, max over reads and XCDs)
+      socket_power_samples_w  the table's current socket power over the reads
+    plus ms per call of fn over the window.  None without amdsmi."""
+    import threading
+    import torch
+    h = _amdsmi_handle()
+    if h is None:
+        return None
+    import amdsmi
+    try:
+        res_uj = float(amdsmi.amdsmi_get_energy_count(h).get("counter_resolution", 15.259))
+    except Exception:  # MI300-series energy unit
+        res_uj = 15.259
+
+    snaps = []  # (host time, metrics table)
+    stop = threading.Event()
+
+    def sample():
+        while not stop.is_set():
+            snaps.append((time.perf_counter(), amdsmi.amdsmi_get_gpu_metrics_info(h)))
+            stop.wait(0.02)
+
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    th = threading.Thread(target=sample, daemon=True)
+    th.start()
+    n = 0
+    while time.perf_counter() - t0 < seconds:
+        fn()
+        n += 1
+        if n % sync_every == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    stop.set()
+    th.join()
+    out = {"seconds": round(t1 - t0, 3), "calls": n, "ms_per_call": round((t1 - t0) * 1e3 / n, 4)}
+    try:
+        out["power_cap_w"] = round(amdsmi.amdsmi_get_power_info(h)["power_limit"] / 1e6, 1)
+    except Exception:  # the cap is informational
+        out["power_cap_w"] = None
+    busy = [m for t, m in snaps if t0 + 0.1 < t < t1]  # past the ramp
+    # distinct table refreshes only (the driver hands out a cached copy in between)
+    uniq = []
+    for m in busy:
+        if not uniq or m.get("system_clock_counter") != uniq[-1].get("system_clock_counter"):
+            uniq.append(m)
+    out["table_refreshes"] = len(uniq)
+    if len(uniq) >= 2:
+        ma, mb = uniq[0], uniq[-1]
+
+        def d(k):
+            x, y = _metric(ma, k), _metric(mb, k)
+            return None if x is None or y is None else y - x
+
+        dt_ns, de = d("system_clock_counter"), d("energy_accumulator")
+        if dt_ns and de is not None:
+            out["power_w"] = round(de * res_uj * 1e-6 / (dt_ns * 1e-9), 1)
+        da = d("accumulation_counter")
+        if da:
+            out["residency"] = {k: round(d(k + "_residency_acc") / da, 3)
+                                for k in ("ppt", "prochot", "socket_thm", "vr_thm", "hbm_thm")
+                                if d(k + "_residency_acc") is not None}
+            for name, key in (("xcd_below_host_limit", "gfx_below_host_limit_total_acc"),
+                              ("xcd_below_host_limit_ppt", "gfx_below_host_limit_ppt_acc"),
+                              ("xcd_below_host_limit_thm", "gfx_below_host_limit_thm_acc"),
+                              ("xcd_low_utilization", "gfx_low_utilization_acc")):
+                k = "xcp_stats." + key
+                if isinstance(ma.get(k), list) and isinstance(mb.get(k), list):
+                    v = [round((y - x) / da, 3) for x, y in zip(ma[k][0], mb[k][0])
+                         if isinstance(x, int) and isinstance(y, int)]
+                    if v:
+                        out[name] = v
+    powers = [p for p in (_metric(m, "current_socket_power") for m in uniq) if p is not None]
+    clocks = [x for m in busy for x in (m.get("current_gfxclks") or [])
+              if isinstance(x, (int, float))]
+    if powers:
+        out["socket_power_samples_w"] = {"mean": round(sum(powers) / len(powers), 1),
+                                         "max": max(powers), "n": len(powers)}
+    if clocks:
+        out["gfxclk_mhz"] = {"mean": round(sum(clocks) / len(clocks), 1), "min": min(clocks),
+                             "max": max(clocks), "n": len(clocks)}
+    return out
+
+
+def bench_power_stages(args):
+    """Each stage of the config-4 forward alone, on its config-4 shapes (M =
+    16 x 8192 rows), run back to back for --stage-s seconds under
+    telemetry_window: socket power, PPT residency and XCD clocks per stage,
+    beside the MFMA loop probe (the matrix cores' power at full load), the
+    device copy probe (HBM at full load) and the whole step.  Tells whether a
+    stage is held by the package power limit and at what clock it runs."""
+    import torch
+    from blt_burn_amd import _lib, model as M, patcher, synth
+    L = _lib.lib()
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream().cuda_stream
+    B, T, W, D, F, Hh = args.batch, args.seq, args.window, 768, 2048, 12
+    Mr = B * T
+    g = torch.Generator(device=dev)
+    g.manual_seed(synth.config_seed(4))
+
+    def rnd(shape, std=1.0):
+        return (torch.randn(shape, generator=g, device=dev) * std).to(torch.bfloat16)
+
+    a768, h2048, qkv, attn = rnd((Mr, D)), rnd((Mr, F)), rnd((Mr, 3 * D)), rnd((Mr, D))
+    w13, wqkv, wo, w2 = rnd((2 * F, D), 0.02), rnd((3 * D, D), 0.02), rnd((D, D), 0.02), \
+        rnd((D, F), 0.02)
+    resid = torch.randn((Mr, D), generator=g, device=dev)
+    hout, qout = torch.empty((Mr, F), dtype=torch.bfloat16, device=dev), \
+        torch.empty((Mr, 3 * D), dtype=torch.bfloat16, device=dev)
+    cs = torch.empty((T, 32, 2), dtype=torch.float32, device=dev)
+    _lib.check(L.blt_rope_table_f32(cs.data_ptr(), 64, T, 10000.0, stream), "rope_table")
+
+    def gemm(A, Bt, C, N, K, ldc, epi, rope_cols=0):
+        _lib.check(L.blt_gemm_bf16_epilogue(A.data_ptr(), Bt.data_ptr(), C.data_ptr(), Mr, N, K,
+                                            K, K, ldc, epi, 0, rope_cols, T,
+                                            cs.data_ptr() if rope_cols else None, stream), "gemm")
+
+    def attention():
+        _lib.check(L.blt_fused_attention_bf16(
+            qkv.data_ptr(), qkv[:, D:].data_ptr(), qkv[:, 2 * D:].data_ptr(), attn.data_ptr(),
+            B, Hh, T, 64, T * 3 * D, 64, 3 * D, T * 3 * D, 64, 3 * D, T * D, 64, D, 1, W, 0.0,
+            None, stream), "attention")
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.empty(cus * 4 * 256, device=dev)
+    src = torch.ones((1 << 30) // 4, device=dev)
+    dst = torch.empty_like(src)
+    cfg = M.entropy_model_config()
+    seed = synth.config_seed(4)
+    model = M.LMTransformer(cfg, M.random_weights(cfg, seed, hidden=F), device=0,
+                            max_tokens=Mr, window=W)
+    tok = torch.from_numpy(synth.tokens(seed, (B, T))).to(dev)
+    outs = {n: torch.empty(sh, dtype=torch.float32, device=dev) for n, sh in
+            (("logits", (B, T, 260)), ("pre_norm_embeddings", (B, T, D)),
+             ("embedding_norms", (B, T)), ("entropies", (B, T)), ("coherence_scores", (B, T)))}
+
+    def step():
+        o = model.forward_with_embeddings(tok, out=outs)
+        patcher.patch_boundaries(o.entropies, args.threshold, patcher.PATCH_MONOTONIC)
+
+    stages = [
+        ("w13_gemm_silu", lambda: gemm(a768, w13, hout, 2 * F, D, F, _lib.EPI_SILU_GATE), 8),
+        ("qkv_gemm_rope", lambda: gemm(a768, wqkv, qout, 3 * D, D, 3 * D, _lib.EPI_QKV_ROPE,
+                                       2 * D), 8),
+        ("w2_gemm_residual", lambda: gemm(h2048, w2, resid, D, F, D, _lib.EPI_RESID_F32), 8),
+        ("o_gemm_residual", lambda: gemm(attn, wo, resid, D, D, D, _lib.EPI_RESID_F32), 8),
+        ("attention", attention, 8),
+        ("mfma_probe", lambda: _lib.check(L.blt_probe_mfma_bf16(cus * 4, 2048, sink.data_ptr(),
+                                                                stream), "probe"), 8),
+        ("copy_probe", lambda: _lib.check(L.blt_probe_copy(src.data_ptr(), dst.data_ptr(),
+                                                           1 << 30, stream), "copy"), 8),
+        ("step", step, 2),
+    ]
+    res = {}
+    for name, fn, sync_every in stages:
+        print("power stage %s" % name, file=sys.stderr, flush=True)
+        res[name] = telemetry_window(fn, args.stage_s, sync_every=sync_every)
+        res[name]["event_ms"] = round(_timed(fn, 10, 2), 4)
+    print(json.dumps({"power_stages": res, "shapes": {"rows": Mr, "dim": D, "ffn": F,
+                                                     "heads": Hh, "window": W}}), flush=True)
 
 
 def _cpu_cores():
