@@ -118,8 +118,8 @@ int Model::read_profile(double* ms, int64_t* launches, int n) {
 
 Model::~Model() {
   for (hipEvent_t e : ev_pool) (void)hipEventDestroy(e);
-  void* ptrs[] = {emb, final_norm, attn_nw, ffn_nw, wqkv,  wo,     w13, w2,   wout, rope_cs,
-                  x,   a,          ss,      rstd,   qkv,   attn,   hbuf, logits, ent, norms};
+  void* ptrs[] = {emb, final_norm, attn_nw, ffn_nw, wqkv, wo,   w13,  w2,     wout, wout_head,
+                  rope_cs, x,     a,       ss,     rstd, qkv,  attn, hbuf, logits, ent, norms};
   int prev = -1;
   (void)hipGetDevice(&prev);
   (void)hipSetDevice(device);
@@ -167,6 +167,7 @@ int Model::create(int dev, const blt_model_config& c, const blt_model_weights& w
   rc |= dalloc(&m->w13, L * 2 * F * D, &tb);
   rc |= dalloc(&m->w2, L * D * F, &tb);
   rc |= dalloc(&m->wout, V * D, &tb);
+  if (head_fused_ok((int)D, (int)V)) rc |= dalloc(&m->wout_head, head_packed_elems((int)D), &tb);
   rc |= dalloc(&m->rope_cs, (int64_t)c.max_seqlen * 64, &tb);
   rc |= dalloc(&m->x, max_tok * D, &tb);
   rc |= dalloc(&m->a, max_tok * D, &tb);
@@ -205,6 +206,11 @@ int Model::create(int dev, const blt_model_config& c, const blt_model_weights& w
     std::vector<uint16_t> t(V * D);
     transpose_into(t.data(), w.output, D, V);
     if ((rc = up(m->wout, t.data(), V * D * 2))) { delete m; return rc; }
+    if (m->wout_head) {
+      std::vector<uint16_t> hp(head_packed_elems((int)D));
+      pack_head_weights(t.data(), (int)V, (int)D, hp.data());
+      if ((rc = up(m->wout_head, hp.data(), (int64_t)hp.size() * 2))) { delete m; return rc; }
+    }
   }
   if (L > 0) {
     std::vector<float> f = to_f32(w.attention_norm, L * D);
@@ -335,6 +341,15 @@ int Model::forward(const int32_t* tokens, int64_t B, int64_t T, const blt_model_
     }
     return 0;
   }
+  float* en = o.entropies ? o.entropies : ent;
+  if (wout_head) {
+    // final RMSNorm, pre-norm L2, head (split-bf16 input), entropy and
+    // coherence in one pass over the residual; logits only when asked for
+    if ((rc = launch_head_entropy(xr, final_norm, wout_head, M, (int)D, (int)V, cfg.norm_eps,
+                                  o.logits, en, nr, o.coherence_scores, s)))
+      return rc;
+    return mark(BLT_STAGE_HEAD_GEMM, s);
+  }
   // pre-norm L2 norms fused with the final RMSNorm (one read of the residual)
   if ((rc = launch_rmsnorm<float, float, uint16_t>(xr, final_norm, a, nr, M, (int)D, cfg.norm_eps,
                                                    0, s)))
@@ -346,7 +361,6 @@ int Model::forward(const int32_t* tokens, int64_t B, int64_t T, const blt_model_
   g.M = M; g.N = V; g.K = D; g.lda = D; g.ldb = D; g.ldc = V; g.epi = EPI_F32; g.n_valid = (int)V;
   if ((rc = launch_gemm(g, s))) return rc;
   if ((rc = mark(BLT_STAGE_HEAD_GEMM, s))) return rc;
-  float* en = o.entropies ? o.entropies : ent;
   if ((rc = launch_entropy_f32(lg, en, M, (int)V, s))) return rc;
   if ((rc = mark(BLT_STAGE_ENTROPY, s))) return rc;
   if (o.coherence_scores) {

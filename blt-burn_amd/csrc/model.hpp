@@ -25,6 +25,7 @@ struct Model {
   uint16_t* w13 = nullptr;
   uint16_t* w2 = nullptr;
   uint16_t* wout = nullptr;
+  uint16_t* wout_head = nullptr;  // the head's K tiles for the fused head kernel (k_head.hip)
   float* rope_cs = nullptr;
   // workspace
   float* x = nullptr;

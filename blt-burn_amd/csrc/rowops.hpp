@@ -70,6 +70,17 @@ int launch_entropy_patch(const float* logits, int64_t B, int64_t T, int vocab, f
                          int n_rules, const blt_patch_rule* rules, void* ws, int64_t ws_bytes,
                          hipStream_t s);
 
+// k_head.hip: final RMSNorm + pre-norm L2 + head (input split into bf16 hi +
+// lo) + entropy + coherence in one pass over the f32 residual x [M, D].
+// wpacked = pack_head_weights of the transposed head weight Bt [V, D];
+// logits, ent, norms, coh may each be NULL.
+bool head_fused_ok(int dim, int vocab);
+int64_t head_packed_elems(int dim);
+void pack_head_weights(const uint16_t* bt, int V, int D, uint16_t* out);
+int launch_head_entropy(const float* x, const float* w_norm, const uint16_t* wpacked, int64_t M,
+                        int D, int V, float eps, float* logits, float* ent, float* norms,
+                        float* coh, hipStream_t s);
+
 // k_gemm.hip -----------------------------------------------------------------
 // C[M, N] = A[M, K] . Bt[N, K]^T with bf16 operands and f32 accumulation; the
 // epilogue decides what is written.  K % 64 == 0, N % 64 == 0 (Bt padded with

@@ -124,17 +124,28 @@ def bf16_round(x):
     return u.astype(np.uint32).view(np.float32)
 
 
-def model_forward_bf16_operands(cfg, w, tokens, rounding=True):
+ROUNDING_POINTS = ("norm_in", "q", "k", "v", "p", "attn_out", "silu", "head_in")
+
+
+def model_forward_bf16_operands(cfg, w, tokens, rounding=True, points=None):
     """model_forward in float32 with the GEMM and attention operands rounded to
     bf16 where a bf16-MFMA forward must round them: the RMSNorm-weighted
-    activations x * w (the 1 / rms row factor applied to the GEMM output), q
-    (scaled by 1 / sqrt(d) after RoPE), k and v, the softmax numerators P, the
-    attention output, the SiLU-gate product and the final norm's output.  With
-    rounding=False it is the float32 statement of the reference's math."""
+    activations x * w inside the layers (norm_in; the 1 / rms row factor
+    applied to the GEMM output), q (scaled by 1 / sqrt(d) after RoPE), k and v,
+    the softmax numerators P (p), the attention output (attn_out), the
+    SiLU-gate product (silu) and the final norm's output (head_in).  `points`
+    (a subset of ROUNDING_POINTS) rounds only those; rounding=False or an empty
+    set is the float32 statement of the reference's math."""
     D, L, Hn = cfg["dim"], cfg["n_layers"], cfg["n_heads"]
     hd = D // Hn
     eps, theta, window = cfg["norm_eps"], cfg["rope_theta"], cfg.get("window", 0)
-    r = bf16_round if rounding else (lambda t: np.asarray(t, np.float32))
+    if points is None:
+        points = ROUNDING_POINTS if rounding else ()
+    unknown = set(points) - set(ROUNDING_POINTS)
+    assert not unknown, unknown
+
+    def rp(name):
+        return bf16_round if name in points else (lambda t: np.asarray(t, np.float32))
     W = {k: np.asarray(v, np.float32) for k, v in w.items()}
     tokens = np.asarray(tokens)
     B, T = tokens.shape
@@ -154,16 +165,16 @@ def model_forward_bf16_operands(cfg, w, tokens, rounding=True):
     mask = mask_matrix(T, True, window).astype(np.float32)
     x = W["emb"][tokens]
     for l in range(L):
-        a, f = r(x * W["attn_norm"][l]), rstd(x)
-        q = r(rot(heads((a @ W["wq"][l]) * f)) / np.float32(np.sqrt(hd)))
-        k = r(rot(heads((a @ W["wk"][l]) * f)))
-        v = r(heads((a @ W["wv"][l]) * f))
+        a, f = rp("norm_in")(x * W["attn_norm"][l]), rstd(x)
+        q = rp("q")(rot(heads((a @ W["wq"][l]) * f)) / np.float32(np.sqrt(hd)))
+        k = rp("k")(rot(heads((a @ W["wk"][l]) * f)))
+        v = rp("v")(heads((a @ W["wv"][l]) * f))
         sc = q @ np.swapaxes(k, -1, -2) + mask
-        p = r(np.exp(sc - sc.max(-1, keepdims=True)))
+        p = rp("p")(np.exp(sc - sc.max(-1, keepdims=True)))
         o = (p @ v) / p.sum(-1, keepdims=True)
-        x = x + r(o.transpose(0, 2, 1, 3).reshape(B, T, D)) @ W["wo"][l]
-        a, f = r(x * W["ffn_norm"][l]), rstd(x)
+        x = x + rp("attn_out")(o.transpose(0, 2, 1, 3).reshape(B, T, D)) @ W["wo"][l]
+        a, f = rp("norm_in")(x * W["ffn_norm"][l]), rstd(x)
         g, u = (a @ W["w1"][l]) * f, (a @ W["w3"][l]) * f
-        x = x + r(g / (1 + np.exp(-g)) * u) @ W["w2"][l]
-    logits = r(x * rstd(x) * W["norm"]) @ W["out"]
+        x = x + rp("silu")(g / (1 + np.exp(-g)) * u) @ W["w2"][l]
+    logits = rp("head_in")(x * rstd(x) * W["norm"]) @ W["out"]
     return {"logits": logits, "pre_norm_embeddings": x, "entropies": entropy(logits)}
