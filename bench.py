@@ -56,6 +56,9 @@ def _dispatch_stages(names, layers):
             g += 1
         elif "attn_fwd_kernel" in n:
             out.append("attention")
+        elif "head_entropy_kernel" in n:
+            # the fused final RMSNorm + L2 + head + entropy (+ coherence)
+            out.append("head_gemm")
         elif "rmsnorm" in n:
             out.append("rmsnorm")
         elif "entropy_" in n and "_kernel" in n:

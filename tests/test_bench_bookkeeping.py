@@ -41,6 +41,11 @@ def test_dispatch_stages_one_forward():
     assert st[1:15] == layer * 2
     assert st[15:] == ["rmsnorm", "head_gemm", "entropy", "coherence", "patch_boundaries",
                        "patch_boundaries"]
+    # the fused head replaces the final norm, head GEMM, entropy and coherence
+    fused = _forward_names(2)[:15] + [
+        "void blt::(anonymous namespace)::head_entropy_kernel<true>(float const*)",
+        "blt::(anonymous namespace)::patch_flags_kernel(blt::PatchKArgs)"]
+    assert bench._dispatch_stages(fused, 2)[15:] == ["head_gemm", "patch_boundaries"]
     assert bench._dispatch_stages(["blt::(anonymous namespace)::mfma_peak_kernel(int, float*)",
                                    "at::native::copy"], 2) == [None, None]
 
