@@ -5,7 +5,7 @@ of libblt_hip.so (include/blt_hip.h).  Import-time work is limited to Python;
 the library is loaded on first use and a missing build raises BltError.
 """
 from ._lib import BltError, LIB_PATH, lib, last_error  # noqa: F401
-from . import safetensors_io, synth, tokenizer  # noqa: F401
+from . import mpk_io, safetensors_io, synth, tokenizer  # noqa: F401
 
 __version__ = "0.1.0"
 

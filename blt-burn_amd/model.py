@@ -116,6 +116,27 @@ class LMTransformer:
         entropy_model_config() and the FFN width comes from the file."""
         from .safetensors_io import load_entropy_weights
         w, shp = load_entropy_weights(path)
+        return cls._from_loaded(path, w, shp, cfg, device, max_tokens, window)
+
+    @classmethod
+    def from_mpk(cls, path, cfg=None, device=0, max_tokens=None, window=0):
+        """load_entropy_model's `.mpk` branch (model_loader.rs:119-125): a Burn
+        NamedMpkFileRecorder record of the module, Linear weights already in
+        Burn's [d_input, d_output] layout."""
+        from .mpk_io import load_entropy_weights_mpk
+        w, shp = load_entropy_weights_mpk(path)
+        return cls._from_loaded(path, w, shp, cfg, device, max_tokens, window)
+
+    @classmethod
+    def from_checkpoint(cls, path, cfg=None, device=0, max_tokens=None, window=0):
+        """load_entropy_model (model_loader.rs:103-145): the format follows the
+        file name, `.mpk` for a Burn record and safetensors otherwise."""
+        if str(path).endswith(".mpk"):
+            return cls.from_mpk(path, cfg, device, max_tokens, window)
+        return cls.from_safetensors(path, cfg, device, max_tokens, window)
+
+    @classmethod
+    def _from_loaded(cls, path, w, shp, cfg, device, max_tokens, window):
         cfg = cfg or entropy_model_config()
         if (cfg.dim, cfg.n_layers, cfg.vocab_size) != (shp["dim"], shp["n_layers"], shp["vocab"]):
             raise BltError("checkpoint %s holds dim %d, %d layers, vocab %d; the config says "

@@ -278,3 +278,26 @@ def test_from_safetensors_matches_in_memory_weights(tmp_path):
     bad = M.LMTransformerConfig(dim=128, n_layers=3, n_heads=2, max_seqlen=256)
     with pytest.raises(M.BltError):
         M.LMTransformer.from_safetensors(path, bad, device=0, max_tokens=200)
+
+
+def test_from_mpk_matches_in_memory_weights(tmp_path):
+    """A Burn NamedMpkFileRecorder record (model_loader.rs:119-125: the `.mpk`
+    branch, Linear weights in Burn's [d_input, d_output] layout) loads to the
+    same model as the in-memory weights, through from_mpk and through
+    from_checkpoint's file-name dispatch; outputs are bit-identical."""
+    pytest.importorskip("msgpack")
+    from blt_burn_amd import mpk_io
+    cfg = M.LMTransformerConfig(dim=128, n_layers=2, n_heads=2, ffn_dim_multiplier=1.0,
+                                multiple_of=64, max_seqlen=256, vocab_size=260)
+    w = M.random_weights(cfg, 12, hidden=384)
+    path = str(tmp_path / "blt_entropy_model.mpk")
+    mpk_io.save_entropy_weights_mpk(path, w)
+    tok = torch.from_numpy(synth.tokens(synth.config_seed(4), (2, 100))).cuda()
+    a = M.LMTransformer(cfg, w, device=0, max_tokens=200).forward_with_embeddings(tok)
+    for load in (M.LMTransformer.from_mpk, M.LMTransformer.from_checkpoint):
+        mb = load(path, cfg, device=0, max_tokens=200)
+        assert mb.hidden == 384
+        b = mb.forward_with_embeddings(tok)
+        torch.cuda.synchronize()
+        for n in ("logits", "pre_norm_embeddings", "embedding_norms", "entropies"):
+            assert torch.equal(getattr(a, n), getattr(b, n)), n
