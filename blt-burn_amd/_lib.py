@@ -124,13 +124,15 @@ class PatchRule(ctypes.Structure):
 class IngestStats(ctypes.Structure):
     """blt_ingest_stats."""
     _fields_ = [("batches", c_i64), ("documents", c_i64), ("tokens", c_i64),
-                ("tokens_computed", c_i64), ("row_tokens", c_i64)]
+                ("tokens_computed", c_i64), ("row_tokens", c_i64), ("long_documents", c_i64),
+                ("long_documents_host", c_i64)]
 
 
 class IngestConfig(ctypes.Structure):
     """blt_ingest_config."""
     _fields_ = [("rows", c_i32), ("row_len", c_i32), ("chunk_len", c_i32), ("overlap", c_i32),
-                ("threshold", c_f32), ("mode", c_i32), ("with_embeddings", c_i32)]
+                ("threshold", c_f32), ("mode", c_i32), ("with_embeddings", c_i32),
+                ("long_arena_tokens", c_i32)]
 
 
 _lib = None

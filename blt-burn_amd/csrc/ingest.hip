@@ -94,10 +94,17 @@ struct Unit {
   bool whole;
 };
 
-// Host gather of a document that spans batches: stitched entropies / norms /
-// coherence until its last unit lands.
+// A document that spans batches.  Its pieces are stitched into a range of the
+// device arena (slot >= 0): each batch copies its pieces there on the compute
+// stream, and the batch holding the last one also runs the document's boundary
+// pass and per-patch means there and downloads them with its own outputs.  A
+// document the arena cannot hold (slot < 0) is gathered on the host until its
+// last unit lands, then takes a synchronous pass of its own.
 struct LongDoc {
-  int64_t remaining = 0;  // units not yet finished
+  int64_t remaining = 0;  // units not yet stitched (arena) / finished (host)
+  int64_t L = 0;
+  int32_t slot = -1;      // arena document slot, -1: host gather, -2: not placed yet
+  int64_t base = 0;       // the document's first token in the arena
   std::vector<float> H, N, C;
 };
 
@@ -149,7 +156,40 @@ struct Ingest {
     bool busy = false;
     std::vector<int64_t> units;  // ids of the units in this batch
     int64_t out_tokens = 0;      // outputs of those units
+    std::vector<int64_t> long_done;  // arena documents completed by this batch
   } slot[2];
+
+  // Device arena of the documents that span batches (allocated at first use,
+  // la_cap tokens and kArenaDocs document slots), its pinned result copies, and
+  // a first-fit list of the token ranges in use (base -> length).
+  static constexpr int32_t kArenaDocs = 64;
+  int64_t la_cap = 0;
+  float* la_H = nullptr;
+  float* la_N = nullptr;
+  float* la_C = nullptr;
+  float* la_pH = nullptr;
+  float* la_pN = nullptr;
+  float* la_pC = nullptr;
+  int32_t* la_starts = nullptr;
+  int32_t* la_lens = nullptr;
+  int64_t* la_off = nullptr;  // [kArenaDocs]
+  int32_t* la_len = nullptr;
+  int32_t* la_count = nullptr;
+  int32_t* lh_starts = nullptr;
+  int32_t* lh_lens = nullptr;
+  float* lh_pH = nullptr;
+  float* lh_pN = nullptr;
+  float* lh_pC = nullptr;
+  int64_t* lh_off = nullptr;  // [kArenaDocs]
+  int32_t* lh_len = nullptr;
+  int32_t* lh_count = nullptr;
+  std::map<int64_t, int64_t> la_used;
+  std::vector<char> la_slot_used;
+  int64_t arena_tokens() const;
+  int ensure_arena();
+  // places a document in the arena (slot >= 0) or leaves it to the host pass
+  int place_long(LongDoc& ld);
+  void release_long(LongDoc& ld);
 
   // this run's packing units and the documents that span batches
   std::vector<Unit> units;
@@ -205,9 +245,14 @@ Ingest::~Ingest() {
     for (hipEvent_t e : {s.uploaded, s.computed, s.done})
       if (e) (void)hipEventDestroy(e);
   }
-  void* lp[] = {l_H, l_N, l_C, l_starts, l_lens, l_pH, l_pN, l_pC, l_off, l_len, l_count};
+  void* lp[] = {l_H, l_N, l_C, l_starts, l_lens, l_pH, l_pN, l_pC, l_off, l_len, l_count,
+                la_H, la_N, la_C, la_pH, la_pN, la_pC, la_starts, la_lens, la_off, la_len,
+                la_count};
   for (void* p : lp)
     if (p) (void)hipFree(p);
+  void* hp[] = {lh_starts, lh_lens, lh_pH, lh_pN, lh_pC, lh_off, lh_len, lh_count};
+  for (void* p : hp)
+    if (p) (void)hipHostFree(p);
   for (hipStream_t st : {up, ks, down})
     if (st) (void)hipStreamDestroy(st);
 }
@@ -218,7 +263,90 @@ void Ingest::drain() {
     s.busy = false;
     s.units.clear();
     s.out_tokens = 0;
+    s.long_done.clear();
   }
+  la_used.clear();
+  std::fill(la_slot_used.begin(), la_slot_used.end(), 0);
+}
+
+// Arena capacity in tokens: long_arena_tokens, 2^22 when 0, none when negative.
+int64_t Ingest::arena_tokens() const {
+  if (cfg.long_arena_tokens < 0) return 0;
+  return cfg.long_arena_tokens > 0 ? (int64_t)cfg.long_arena_tokens : ((int64_t)1 << 22);
+}
+
+int Ingest::ensure_arena() {
+  if (la_cap > 0) return 0;
+  const int64_t n = arena_tokens();
+  const size_t b = (size_t)n * 4;
+  BLT_HIP_CHECK(hipMalloc((void**)&la_H, b));
+  BLT_HIP_CHECK(hipMalloc((void**)&la_N, b));
+  BLT_HIP_CHECK(hipMalloc((void**)&la_C, b));
+  BLT_HIP_CHECK(hipMalloc((void**)&la_pH, b));
+  BLT_HIP_CHECK(hipMalloc((void**)&la_pN, b));
+  BLT_HIP_CHECK(hipMalloc((void**)&la_pC, b));
+  BLT_HIP_CHECK(hipMalloc((void**)&la_starts, b));
+  BLT_HIP_CHECK(hipMalloc((void**)&la_lens, b));
+  BLT_HIP_CHECK(hipMalloc((void**)&la_off, kArenaDocs * 8));
+  BLT_HIP_CHECK(hipMalloc((void**)&la_len, kArenaDocs * 4));
+  BLT_HIP_CHECK(hipMalloc((void**)&la_count, kArenaDocs * 4));
+  BLT_HIP_CHECK(hipHostMalloc((void**)&lh_starts, b, 0));
+  BLT_HIP_CHECK(hipHostMalloc((void**)&lh_lens, b, 0));
+  BLT_HIP_CHECK(hipHostMalloc((void**)&lh_pH, b, 0));
+  BLT_HIP_CHECK(hipHostMalloc((void**)&lh_pN, b, 0));
+  BLT_HIP_CHECK(hipHostMalloc((void**)&lh_pC, b, 0));
+  BLT_HIP_CHECK(hipHostMalloc((void**)&lh_off, kArenaDocs * 8, 0));
+  BLT_HIP_CHECK(hipHostMalloc((void**)&lh_len, kArenaDocs * 4, 0));
+  BLT_HIP_CHECK(hipHostMalloc((void**)&lh_count, kArenaDocs * 4, 0));
+  la_slot_used.assign(kArenaDocs, 0);
+  la_cap = n;
+  return 0;
+}
+
+// First fit over the arena's free token ranges.  The offset / length words of
+// the document's slot go up on the compute stream, ahead of its pieces.  A
+// slot's words and range are only rewritten after finish() has waited for the
+// batch that completed its previous document.
+int Ingest::place_long(LongDoc& ld) {
+  ld.slot = -1;
+  const int64_t cap = arena_tokens();
+  if (ld.L <= 0 || ld.L > cap) return 0;
+  int rc;
+  if ((rc = ensure_arena())) return rc;
+  int32_t sl = -1;
+  for (int32_t i = 0; i < kArenaDocs; ++i)
+    if (!la_slot_used[(size_t)i]) {
+      sl = i;
+      break;
+    }
+  if (sl < 0) return 0;
+  int64_t at = 0;
+  bool found = false;
+  for (const auto& r : la_used) {
+    if (r.first - at >= ld.L) {
+      found = true;
+      break;
+    }
+    at = r.first + r.second;
+  }
+  if (!found && la_cap - at < ld.L) return 0;
+  la_used[at] = ld.L;
+  la_slot_used[(size_t)sl] = 1;
+  ld.slot = sl;
+  ld.base = at;
+  lh_off[sl] = at;
+  lh_len[sl] = (int32_t)ld.L;
+  BLT_HIP_CHECK(hipMemcpyAsync(la_off + sl, lh_off + sl, 8, hipMemcpyHostToDevice, ks));
+  BLT_HIP_CHECK(hipMemcpyAsync(la_len + sl, lh_len + sl, 4, hipMemcpyHostToDevice, ks));
+  return 0;
+}
+
+void Ingest::release_long(LongDoc& ld) {
+  if (ld.slot >= 0) {
+    la_used.erase(ld.base);
+    la_slot_used[(size_t)ld.slot] = 0;
+  }
+  ld = LongDoc{};
 }
 
 int Ingest::ensure_long(int64_t L) {
@@ -358,6 +486,10 @@ int Ingest::finish(Slot& s, const int64_t* doc_off, float* ent, float* nrm, floa
     if (emb && s.h_E) memcpy(emb + dst * dim, s.h_E + src * dim, (size_t)(L * dim) * 4);
     if (!u.whole) {
       LongDoc& ld = longs[d];
+      if (ld.slot >= 0) continue;  // stitched on the device
+      if (ld.slot != -1 || (int64_t)ld.H.size() < u.out_lo + L ||
+          (pm.any() && ((int64_t)ld.N.size() < u.out_lo + L || (int64_t)ld.C.size() < u.out_lo + L)))
+        return fail(BLT_ERR_HIP, "ingest_run: a long document's piece has no host buffer");
       memcpy(ld.H.data() + u.out_lo, s.h_H + src, (size_t)L * 4);
       if (pm.any()) {
         memcpy(ld.N.data() + u.out_lo, s.h_N + src, (size_t)L * 4);
@@ -377,6 +509,20 @@ int Ingest::finish(Slot& s, const int64_t* doc_off, float* ent, float* nrm, floa
     if (pm.coh) memcpy(pm.coh + dst, s.h_pC + src, (size_t)n * 4);
     if (counts) counts[d] = n;
   }
+  for (int64_t d : s.long_done) {
+    LongDoc& ld = longs[d];
+    const int32_t n = lh_count[ld.slot];
+    if (n < 0 || n > ld.L) return fail(BLT_ERR_HIP, "ingest_run: bad patch count");
+    const int64_t dst = doc_off[d], b0 = ld.base;
+    if (starts) memcpy(starts + dst, lh_starts + b0, (size_t)n * 4);
+    if (lens) memcpy(lens + dst, lh_lens + b0, (size_t)n * 4);
+    if (pm.ent) memcpy(pm.ent + dst, lh_pH + b0, (size_t)n * 4);
+    if (pm.prom) memcpy(pm.prom + dst, lh_pN + b0, (size_t)n * 4);
+    if (pm.coh) memcpy(pm.coh + dst, lh_pC + b0, (size_t)n * 4);
+    if (counts) counts[d] = n;
+    release_long(ld);
+  }
+  s.long_done.clear();
   return 0;
 }
 
@@ -437,11 +583,9 @@ int Ingest::run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, f
     }
     LongDoc& ld = longs[d];
     ld.remaining = nu;
-    ld.H.assign((size_t)L, 0.f);
-    if (pm.any()) {
-      ld.N.assign((size_t)L, 0.f);
-      ld.C.assign((size_t)L, 0.f);
-    }
+    ld.L = L;
+    ld.slot = -2;  // placed when its first unit is packed
+    stats.long_documents += 1;
   }
   BLT_HIP_CHECK(hipSetDevice(m->device));
   std::vector<char> taken(units.size(), 0);
@@ -453,6 +597,7 @@ int Ingest::run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, f
     std::fill(fill.begin(), fill.end(), 0);
     s.units.clear();
     s.out_tokens = 0;
+    s.long_done.clear();
     // ---- pack units: the oldest pending one first (it always fits an empty
     // batch), then any of the next kLookahead that still fit ----
     int64_t free_tokens = BT;
@@ -466,6 +611,20 @@ int Ingest::run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, f
       sub.assign(chunks.begin() + u.c0, chunks.begin() + u.c1);
       if (!pack_chunks(sub, fill, T, order, row, col)) continue;
       taken[i] = 1;
+      if (!u.whole) {
+        LongDoc& ld = longs[u.doc];
+        if (ld.slot == -2) {
+          if ((rc = place_long(ld))) return rc;
+          if (ld.slot < 0) {  // the host gathers it
+            stats.long_documents_host += 1;
+            ld.H.assign((size_t)ld.L, 0.f);
+            if (pm.any()) {
+              ld.N.assign((size_t)ld.L, 0.f);
+              ld.C.assign((size_t)ld.L, 0.f);
+            }
+          }
+        }
+      }
       const int64_t jd = (int64_t)s.units.size();
       s.h_doff[jd] = s.out_tokens;
       s.h_dlen[jd] = (int32_t)u.out_len;
@@ -525,6 +684,35 @@ int Ingest::run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, f
     if (pm.any() && (rc = launch_patch_means(s.d_H, s.d_N, s.d_C, s.d_starts, s.d_counts, nd, 0,
                                              s.d_doff, s.d_dlen, s.d_pH, s.d_pN, s.d_pC, ks)))
       return rc;
+    // pieces of arena documents: stitched on the device; the batch holding a
+    // document's last piece runs its boundary pass and per-patch means
+    for (size_t j = 0; j < s.units.size(); ++j) {
+      const Unit& u = units[(size_t)s.units[j]];
+      if (u.whole) continue;
+      LongDoc& ld = longs[u.doc];
+      if (ld.slot < 0) continue;
+      const int64_t src = s.h_doff[j];
+      if (u.out_lo < 0 || u.out_len < 0 || u.out_lo + u.out_len > ld.L || src < 0 ||
+          src + u.out_len > s.out_tokens || ld.base + ld.L > la_cap)
+        return fail(BLT_ERR_HIP, "ingest_run: a long document's piece is out of range");
+      const size_t nbytes = (size_t)u.out_len * 4;
+      const int64_t at = ld.base + u.out_lo;
+      BLT_HIP_CHECK(hipMemcpyAsync(la_H + at, s.d_H + src, nbytes, hipMemcpyDeviceToDevice, ks));
+      if (pm.any()) {
+        BLT_HIP_CHECK(hipMemcpyAsync(la_N + at, s.d_N + src, nbytes, hipMemcpyDeviceToDevice, ks));
+        BLT_HIP_CHECK(hipMemcpyAsync(la_C + at, s.d_C + src, nbytes, hipMemcpyDeviceToDevice, ks));
+      }
+      if (--ld.remaining > 0) continue;
+      if ((rc = launch_patch_boundaries_varlen(la_H, la_off + ld.slot, la_len + ld.slot, 1,
+                                               cfg.threshold, cfg.mode, nullptr, la_starts,
+                                               la_lens, la_count + ld.slot, ks)))
+        return rc;
+      if (pm.any() &&
+          (rc = launch_patch_means(la_H, la_N, la_C, la_starts, la_count + ld.slot, 1, 0,
+                                   la_off + ld.slot, la_len + ld.slot, la_pH, la_pN, la_pC, ks)))
+        return rc;
+      s.long_done.push_back(u.doc);
+    }
     BLT_HIP_CHECK(hipEventRecord(s.computed, ks));
     // ---- download ----
     BLT_HIP_CHECK(hipStreamWaitEvent(down, s.computed, 0));
@@ -541,12 +729,28 @@ int Ingest::run(const int32_t* tokens, const int64_t* doc_off, int64_t n_docs, f
     if (pm.ent) BLT_HIP_CHECK(hipMemcpyAsync(s.h_pH, s.d_pH, ob, hipMemcpyDeviceToHost, down));
     if (pm.prom) BLT_HIP_CHECK(hipMemcpyAsync(s.h_pN, s.d_pN, ob, hipMemcpyDeviceToHost, down));
     if (pm.coh) BLT_HIP_CHECK(hipMemcpyAsync(s.h_pC, s.d_pC, ob, hipMemcpyDeviceToHost, down));
+    for (int64_t d : s.long_done) {
+      const LongDoc& ld = longs[d];
+      const size_t lb = (size_t)ld.L * 4;
+      const int64_t b0 = ld.base;
+      BLT_HIP_CHECK(hipMemcpyAsync(lh_count + ld.slot, la_count + ld.slot, 4,
+                                   hipMemcpyDeviceToHost, down));
+      if (starts)
+        BLT_HIP_CHECK(hipMemcpyAsync(lh_starts + b0, la_starts + b0, lb, hipMemcpyDeviceToHost, down));
+      if (lens)
+        BLT_HIP_CHECK(hipMemcpyAsync(lh_lens + b0, la_lens + b0, lb, hipMemcpyDeviceToHost, down));
+      if (pm.ent) BLT_HIP_CHECK(hipMemcpyAsync(lh_pH + b0, la_pH + b0, lb, hipMemcpyDeviceToHost, down));
+      if (pm.prom) BLT_HIP_CHECK(hipMemcpyAsync(lh_pN + b0, la_pN + b0, lb, hipMemcpyDeviceToHost, down));
+      if (pm.coh) BLT_HIP_CHECK(hipMemcpyAsync(lh_pC + b0, la_pC + b0, lb, hipMemcpyDeviceToHost, down));
+    }
     BLT_HIP_CHECK(hipEventRecord(s.done, down));
     s.busy = true;
     k ^= 1;
   }
-  for (Slot& s : slot)
-    if ((rc = finish(s, doc_off, ent, nrm, coh, emb, starts, lens, counts, pm))) return rc;
+  // the older batch first (slot k would take the next one): a document is
+  // released by the batch that holds its last piece, after its earlier pieces
+  for (Slot* s : {&slot[k], &slot[k ^ 1]})
+    if ((rc = finish(*s, doc_off, ent, nrm, coh, emb, starts, lens, counts, pm))) return rc;
   if (counts)
     for (int64_t dd = 0; dd < n_docs; ++dd)
       if (doc_off[dd + 1] == doc_off[dd]) counts[dd] = 0;

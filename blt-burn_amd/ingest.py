@@ -108,10 +108,12 @@ class StreamingIngest:
     chunk_len / overlap / threshold come from `config` (BltConfig), the
     boundary rule from `mode` (the reference's process_bytes always applies
     the monotonic rule, blt_core.rs:118-119, 185-186).  Documents may be of any
-    length: one whose chunks do not fit a batch spans several."""
+    length: one whose chunks do not fit a batch spans several; such a document
+    is stitched on the device in `long_arena_tokens` of room (0: 2^22, negative:
+    none, every such document then gathered on the host)."""
 
     def __init__(self, model, config=None, rows=None, row_len=None, mode=PATCH_MONOTONIC,
-                 with_embeddings=False):
+                 with_embeddings=False, long_arena_tokens=0):
         self.model = model
         self.config = config or BltConfig()
         self.row_len = row_len or max(self.config.max_seq_len,
@@ -121,7 +123,7 @@ class StreamingIngest:
         self.mode = mode
         c = IngestConfig(self.rows, self.row_len, self.config.max_seq_len,
                          self.config.chunk_overlap, float(self.config.threshold), mode,
-                         int(self.with_embeddings))
+                         int(self.with_embeddings), int(long_arena_tokens))
         h = ctypes.c_void_p()
         check(_lib.lib().blt_ingest_create(model._h, ctypes.byref(c), ctypes.byref(h)),
               "blt_ingest_create")

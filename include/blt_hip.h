@@ -369,6 +369,11 @@ typedef struct blt_ingest_config {
   float threshold;         /* BltConfig::threshold */
   int32_t mode;            /* blt_patch_mode (BltConfig::monotonicity) */
   int32_t with_embeddings; /* != 0: return pre-norm embeddings as well */
+  /* device room, in tokens, for documents longer than one batch: their pieces
+   * are stitched and their boundary pass runs on the device.  0 means 2^22; a
+   * negative value means none.  A document the room cannot hold at the time
+   * is gathered on the host and takes a synchronous pass of its own. */
+  int32_t long_arena_tokens;
 } blt_ingest_config;
 typedef struct blt_ingest blt_ingest;
 
@@ -410,6 +415,8 @@ typedef struct blt_ingest_stats {
   int64_t tokens;
   int64_t tokens_computed;
   int64_t row_tokens;
+  int64_t long_documents;       /* documents longer than one batch */
+  int64_t long_documents_host;  /* of those, the ones gathered on the host */
 } blt_ingest_stats;
 int blt_ingest_last_stats(blt_ingest* g, blt_ingest_stats* out);
 

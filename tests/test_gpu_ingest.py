@@ -252,21 +252,50 @@ def test_ingest_rejects_bad_shapes():
     assert res.counts.size == 2 and int(res.lengths[:res.counts[0]].sum()) == 10
 
 
-def test_ingest_long_documents_vs_oracle_tiny():
+_LONG_RUNS = {}
+
+
+@pytest.mark.parametrize("arena", [0, -1, 1100])
+def test_ingest_long_documents_vs_oracle_tiny(arena):
     """Documents whose chunks need more rows than one batch has (the reference
     loops over any number of chunks, blt_core.rs:300-356): they span several
-    batches, are stitched on the host and get their boundary pass and patch
-    means once complete; short documents share the batches with them."""
+    batches and get their boundary pass and patch means once complete; short
+    documents share the batches with them.  arena 0: every such document is
+    stitched on the device; -1: none is (host gather); 1100 tokens: the
+    1000-token document is, the 2049-token one cannot be.  All three give the
+    same outputs bit for bit."""
     cfg = M.LMTransformerConfig(**TINY)
     w = M.random_weights(cfg, 31, hidden=256)
     m = M.LMTransformer(cfg, w, device=0, max_tokens=2 * 128, window=0)
     conf = I.BltConfig(threshold=0.3, max_seq_len=64, chunk_overlap=16)
-    ing = I.StreamingIngest(m, conf, rows=2, row_len=128, with_embeddings=True)
+    ing = I.StreamingIngest(m, conf, rows=2, row_len=128, with_embeddings=True,
+                            long_arena_tokens=arena)
     lens = [1000, 5, 0, 257, 400, 64, 2049, 3]
     toks, off = _docs(synth.config_seed(5) + 12, lens)
     res = ing.run(toks, off, patch_means=True)
     st = ing.last_stats()
     assert st["batches"] > 1 and st["tokens"] == sum(lens)
+    assert st["long_documents"] == 4  # 1000, 257, 400 and 2049 tokens
+    host = st["long_documents_host"]
+    if arena == 0:
+        assert host == 0
+    elif arena < 0:
+        assert host == 4
+    else:
+        assert 1 <= host <= 3
+    _LONG_RUNS[arena] = res
+    if len(_LONG_RUNS) > 1:
+        first = next(iter(_LONG_RUNS.values()))
+        for n in ("entropies", "norms", "coherence", "starts", "lengths", "counts",
+                  "patch_entropy", "patch_prominence", "patch_coherence"):
+            a, b = getattr(first, n), getattr(res, n)
+            if n in ("starts", "lengths", "patch_entropy", "patch_prominence",
+                     "patch_coherence"):  # only the written entries are outputs
+                for d in range(len(lens)):
+                    o, c = int(res.offsets[d]), int(res.counts[d])
+                    assert np.array_equal(a[o:o + c], b[o:o + c]), (n, d)
+            else:
+                assert np.array_equal(a, b), n
     oc, ow = _oracle_cfg(cfg, 256, 0), _oracle_weights(w)
     for d, L in enumerate(lens):
         ref = oracle.process_document(oc, ow, toks[off[d]:off[d + 1]], 64, 16, 0.3)
