@@ -202,6 +202,19 @@ def test_entropy_model_spread_entropies(out_std, std):
         clear[:, :2] = True  # positions 0 and 1 start patches under either rule
         assert 0 < want.sum() < want.size, (mode, want.sum())
         np.testing.assert_array_equal(mask[clear], want[clear])
+    # Starts the GPU moves against the oracle's own under the monotonic rule at
+    # the reference default delta 1.335 (blt_core.rs:73) and at 0.2, beside the
+    # emulation's: positions near the threshold flip, no more than the bf16
+    # operands account for.
+    for thr in (1.335, 0.2):
+        want = oracle.patch_mask(Hr, thr, patcher.PATCH_MONOTONIC)
+        g_d = int((oracle.patch_mask(H, thr, patcher.PATCH_MONOTONIC) != want).sum())
+        e_d = int((oracle.patch_mask(emu["entropies"], thr, patcher.PATCH_MONOTONIC)
+                   != want).sum())
+        print("spread out_std=%g std=%g: delta %g starts differing from the oracle's: "
+              "GPU %d, emulation %d, of %d starts over %d positions"
+              % (out_std, std, thr, g_d, e_d, int(want.sum()), want.size))
+        assert g_d <= 2 * e_d + 2, (thr, g_d, e_d)
 
 
 @pytest.mark.parametrize("vocab", [100, 258])
