@@ -90,6 +90,8 @@ def _tensor(rec, what):
         raw = rec["bytes"]
         if isinstance(raw, (list, tuple)):
             raw = bytes(raw)
+        if not isinstance(raw, (bytes, bytearray)):
+            raise MpkError("%s: tensor bytes of type %s" % (what, type(raw).__name__))
         npdt = np.dtype(_FLOAT_NP[dt])
         if len(raw) != n * npdt.itemsize:
             raise MpkError("%s: %d bytes for shape %s of %s" % (what, len(raw), shape, dt))

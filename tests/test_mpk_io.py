@@ -181,6 +181,10 @@ def test_reader_rejects_bad_records(tmp_path):
     def int_dtype(r):
         r["item"]["norm"]["weight"]["param"]["dtype"] = "I32"
     bad(int_dtype, "non-float")
+
+    def str_bytes(r):
+        r["item"]["norm"]["weight"]["param"]["bytes"] = "not bytes"
+    bad(str_bytes, "tensor bytes of type")
     with open(p, "wb") as f:
         f.write(b"\xc1not msgpack")
     with pytest.raises(mpk_io.MpkError):
