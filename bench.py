@@ -75,6 +75,16 @@ def _dispatch_stages(names, layers):
     return out
 
 
+def _forward_stages(names, layers):
+    """_dispatch_stages over a run's dispatches: the run is split into forwards,
+    each starting at its embed_kernel (dispatches before the first get None)."""
+    starts = [i for i, n in enumerate(names) if "embed_kernel" in n] + [len(names)]
+    out = [None] * starts[0]
+    for a, b in zip(starts[:-1], starts[1:]):
+        out += _dispatch_stages(names[a:b], layers)
+    return out
+
+
 def _read_counter_csv(path, counter):
     import csv
     rows = [r for r in csv.DictReader(open(path)) if r["Counter_Name"] == counter]
@@ -82,24 +92,24 @@ def _read_counter_csv(path, counter):
     return [(r["Kernel_Name"], float(r["Counter_Value"])) for r in rows]
 
 
-def summarize(args):
+def summarize_dirs(dirs, copy_bytes, L=14):
     """Per-stage HBM traffic per launch from rocprofv3 --pmc runs of
     `bench.py --steps 1 --warmup 0 --no-cpu` (FETCH_SIZE and WRITE_SIZE, KiB per
-    dispatch), each scaled by the bytes a copy of --copy-bytes reads/writes
-    divided by what the counter reports for that copy.  Prints JSON."""
+    dispatch), each scaled by the bytes a copy of copy_bytes reads/writes
+    divided by what the counter reports for that copy.  dirs: the output
+    directories of the fetch, write, copy-fetch and copy-write runs."""
     import glob
     find = lambda d: glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)[0]
-    fetch = _read_counter_csv(find(args.summarize[0]), "FETCH_SIZE")
-    write = _read_counter_csv(find(args.summarize[1]), "WRITE_SIZE")
-    cf = max(v for _, v in _read_counter_csv(find(args.summarize[2]), "FETCH_SIZE"))
-    cw = max(v for _, v in _read_counter_csv(find(args.summarize[3]), "WRITE_SIZE"))
-    kf, kw = args.copy_bytes / (cf * 1024.0), args.copy_bytes / (cw * 1024.0)
-    L = 14
-    res = {"fetch_scale": kf, "write_scale": kw, "copy_bytes": args.copy_bytes,
+    fetch = _read_counter_csv(find(dirs[0]), "FETCH_SIZE")
+    write = _read_counter_csv(find(dirs[1]), "WRITE_SIZE")
+    cf = max(v for _, v in _read_counter_csv(find(dirs[2]), "FETCH_SIZE"))
+    cw = max(v for _, v in _read_counter_csv(find(dirs[3]), "WRITE_SIZE"))
+    kf, kw = copy_bytes / (cf * 1024.0), copy_bytes / (cw * 1024.0)
+    res = {"fetch_scale": kf, "write_scale": kw, "copy_bytes": copy_bytes,
            "copy_fetch_kib": cf, "copy_write_kib": cw, "stages": {}}
     for lst, key, k in ((fetch, "fetch_bytes", kf), (write, "write_bytes", kw)):
         ours = [(n, v) for n, v in lst if "blt::" in n]
-        for st, (n, v) in zip(_dispatch_stages([n for n, _ in ours], L), ours):
+        for st, (n, v) in zip(_forward_stages([n for n, _ in ours], L), ours):
             if st is None:
                 continue
             d = res["stages"].setdefault(st, {"launches": 0})
@@ -109,7 +119,59 @@ def summarize(args):
     for d in res["stages"].values():
         for key in ("fetch_bytes", "write_bytes"):
             d[key] = round(d.get(key, 0.0) / max(d["launches"], 1))
-    print(json.dumps(res, indent=1))
+    return res
+
+
+def summarize(args):
+    """--summarize: summarize_dirs of the four given directories as JSON."""
+    print(json.dumps(summarize_dirs(args.summarize, args.copy_bytes), indent=1))
+
+
+def live_traffic(args, timeout_s=180):
+    """Config 4's per-stage traffic measured in this run: the four rocprofv3
+    --pmc passes that --summarize reads (one counter each: FETCH_SIZE, then
+    WRITE_SIZE, over a one-step bench of the same shape, then both over the
+    copy probe), each a child process under its own time limit.  Called
+    before this process touches the GPU.  Returns (summary, None) or
+    (None, reason)."""
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None, "rocprofv3 not on PATH"
+    tmp = tempfile.mkdtemp(prefix="blt_traffic_")
+    step = ["--steps", "1", "--warmup", "0", "--no-cpu", "--telemetry-s", "0",
+            "--traffic", "off", "--batch", str(args.batch), "--seq", str(args.seq),
+            "--window", str(args.window), "--threshold", repr(args.threshold)]
+    probe = ["--copy-probe", "--copy-bytes", repr(args.copy_bytes)]
+    runs = (("tf", "FETCH_SIZE", step), ("tw", "WRITE_SIZE", step),
+            ("cf", "FETCH_SIZE", probe), ("cw", "WRITE_SIZE", probe))
+    try:
+        for d, counter, extra in runs:
+            cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", os.path.join(tmp, d),
+                   "-o", "p", "--", sys.executable, os.path.abspath(__file__)] + extra
+            with open(os.path.join(tmp, d + ".log"), "w") as log:
+                proc = subprocess.Popen(cmd, stdout=log, stderr=subprocess.STDOUT,
+                                        start_new_session=True, cwd=tmp)
+                try:
+                    rc = proc.wait(timeout=timeout_s)
+                except subprocess.TimeoutExpired:
+                    os.killpg(proc.pid, signal.SIGKILL)
+                    proc.wait()
+                    return None, "rocprofv3 --pmc %s timed out after %d s" % (counter, timeout_s)
+            # rocprofv3 can exit non-zero after the program ended with its
+            # results written; the summary below checks they are whole
+            if rc != 0:
+                print("bench: rocprofv3 --pmc %s exited %d" % (counter, rc), file=sys.stderr)
+        try:
+            res = summarize_dirs([os.path.join(tmp, d) for d, _, _ in runs], args.copy_bytes)
+        except (IndexError, KeyError, ValueError, OSError) as e:
+            return None, "no usable counter output (%s: %s)" % (type(e).__name__, e)
+        return res, None
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
 
 
 def summarize_trace(path):
@@ -119,17 +181,14 @@ def summarize_trace(path):
     rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Dispatch_Id"]))
     rows = [r for r in rows if "blt::" in r["Kernel_Name"]]
     names = [r["Kernel_Name"] for r in rows]
-    # split into forwards: each starts with embed_kernel
-    starts = [i for i, n in enumerate(names) if "embed_kernel" in n] + [len(names)]
     agg = {}
-    for a, b in zip(starts[:-1], starts[1:]):
-        for st, r in zip(_dispatch_stages(names[a:b], 14), rows[a:b]):
-            if st is None:
-                continue
-            kn = r["Kernel_Name"]
-            d = agg.setdefault(st, [0, 0.0, kn[:kn.rfind("(")]])
-            d[0] += 1
-            d[1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    for st, r in zip(_forward_stages(names, 14), rows):
+        if st is None:
+            continue
+        kn = r["Kernel_Name"]
+        d = agg.setdefault(st, [0, 0.0, kn[:kn.rfind("(")]])
+        d[0] += 1
+        d[1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
     print("| stage | kernel | launches | mean us | total us |")
     print("|---|---|---|---|---|")
     for st, (n, us, k) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
@@ -176,6 +235,11 @@ def main():
                          "back for --stage-s seconds) with power, PPT residency and clocks; "
                          "one JSON line")
     ap.add_argument("--stage-s", type=float, default=1.5)
+    ap.add_argument("--traffic", choices=("live", "file", "off"), default="live",
+                    help="config 4's roofline.traffic: live = rocprofv3 --pmc passes run by "
+                         "this bench before it starts (about 15 s; the committed file when "
+                         "they fail or when bench.py itself runs under rocprofv3), file = "
+                         "--traffic-file, off = null")
     ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles",
                                                            "traffic_config4.json"),
                     help="per-stage HBM bytes per launch measured with rocprofv3 --pmc")
@@ -210,6 +274,16 @@ def main():
               "share of them with no collective). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
+
+    # config 4's traffic passes run first, while this process has not touched
+    # the GPU (each pass is a child process of its own)
+    live, live_err = None, None
+    if (args.config == 4 and not (args.pipeline or args.power_stages) and args.traffic == "live"
+            and (args.batch, args.seq, args.window) == (16, 8192, 512)):
+        if "ROCPROF_OUTPUT_PATH" in os.environ:
+            live_err = "bench.py runs under rocprofv3"
+        else:
+            live, live_err = live_traffic(args)
 
     import numpy as np
     import torch
@@ -282,15 +356,25 @@ def main():
     ms_tot, launches = mfma_stages[dom]
     per_launch_ms = ms_tot / launches
     achieved = stage_flops(dom, Mtok, B, T, D, F, V, H, W) / (per_launch_ms * 1e-3) / 1e12
-    traffic = None
-    if os.path.exists(args.traffic_file) and (B, T, W) == (16, 8192, 512):
-        st = json.load(open(args.traffic_file)).get("stages", {}).get(dom)
-        if st:
-            traffic = int(st["fetch_bytes"] + st["write_bytes"])
+    traffic, traffic_st, traffic_src = None, None, None
+    if live is not None and (live["stages"].get(dom) or {}).get("launches"):
+        traffic_st = live["stages"][dom]
+        traffic_src = "rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE in this run"
+    elif (args.traffic != "off" and os.path.exists(args.traffic_file)
+          and (B, T, W) == (16, 8192, 512)):
+        traffic_st = json.load(open(args.traffic_file)).get("stages", {}).get(dom)
+        traffic_src = os.path.relpath(args.traffic_file, ROOT) + " (committed)" + (
+            "; live passes: " + live_err if live_err else "")
+    if traffic_st:
+        traffic = int(traffic_st["fetch_bytes"] + traffic_st["write_bytes"])
     roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                 "launch_ms": round(per_launch_ms, 4)}
+    if traffic_st:
+        roofline.update({"traffic_fetch": int(traffic_st["fetch_bytes"]),
+                         "traffic_write": int(traffic_st["write_bytes"]),
+                         "traffic_source": traffic_src})
     step_tflops = total_flops / sec / 1e12
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "bytes/s", "n_gpus": 1,

@@ -249,6 +249,8 @@ __device__ inline void epilogue(const GemmArgs& p, f32x16_t (&acc)[C::TM][C::TN]
 // contiguous run of tile ids, and ids walk groups of group_m M-tiles with M
 // fastest inside a group, so the blocks resident on one XCD share group_m A
 // row-tiles and a few Bt column-tiles in that XCD's L2 (group_m = 0: N fastest).
+// Odd groups walk the column tiles from the last one down, so a group starts
+// on the Bt tiles the previous group ended on.
 template <int BM, int BN>
 __device__ inline void tile_origin(const GemmArgs& p, int bid, int64_t& m0, int64_t& n0) {
   const int ntm = (int)((p.M + BM - 1) / BM), ntn = (int)((p.N + BN - 1) / BN);
@@ -263,6 +265,7 @@ __device__ inline void tile_origin(const GemmArgs& p, int bid, int64_t& m0, int6
     const int local = id - g * gsz;
     tm = first + local % gm;
     tn = local / gm;
+    if (g & 1) tn = ntn - 1 - tn;
   } else {
     tm = id / ntn;
     tn = id % ntn;
@@ -638,7 +641,11 @@ __device__ inline void epilogue_lds(const GemmArgs& p, f32x16_t (&acc)[C::TM][C:
 // through the stage that held the last K tile plus the gap, while the other
 // stage receives the next tile.  Operand rows are addressed as a per-tile
 // uniform base plus a per-lane 32-bit byte offset (the launcher checks that
-// a tile's reach fits).
+// a tile's reach fits).  Tiles whose first column has bit 10 set take their K
+// tiles from the last down (k_rev): an XCD's consecutive rounds of 4 column
+// tiles then alternate direction, and a round starts on the A and Bt K tiles
+// the previous round left in L2 last.  The direction depends on the column
+// only, so an output's K order is the same in every launch shape.
 template <int BM, int BN, int BK, int WM, int WN, int EPI>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_bf16_dma_persistent_kernel(GemmArgs p) {
@@ -731,11 +738,13 @@ void gemm_bf16_dma_persistent_kernel(GemmArgs p) {
   };
 
   const int KT = (int)(p.K / BK);
+  auto k_rev = [](int64_t n) { return (int)((n >> 10) & 1); };
   int64_t m0, n0;
   tile_origin<BM, BN>(p, v, m0, n0);
   set_tile(m0, n0, lane);
   int st = 0;  // stage of the current K tile
-  dma_tile(0, 0);
+  int rev = k_rev(n0);
+  dma_tile(rev ? KT - 1 : 0, 0);
   float rs[C::TM];
   load_row_scales<C>(p, m0 + wm * C::WTM + lrow, rs);
   dma_wait_barrier<0>();
@@ -754,7 +763,7 @@ void gemm_bf16_dma_persistent_kernel(GemmArgs p) {
       // K tile kt + 1, or after the last one the next tile's first (one DMA
       // issue site for both keeps the loop body to one block)
       bool dma_next = true;
-      int kt_next = kt + 1;
+      int kt_next = rev ? KT - 2 - kt : kt + 1;
       if (kt + 1 == KT) {
         kt_next = 0;
         dma_next = more;
@@ -763,6 +772,7 @@ void gemm_bf16_dma_persistent_kernel(GemmArgs p) {
           int ln = lane;
           asm volatile("" : "+v"(ln));
           set_tile(m0n, n0n, ln);
+          kt_next = k_rev(n0n) ? KT - 1 : 0;
         }
       }
       if (EPI == EPI_QKV_ROPE && kt + 1 == KT && n0 + wn * C::WTN < p.rope_cols)
@@ -784,6 +794,7 @@ void gemm_bf16_dma_persistent_kernel(GemmArgs p) {
     v = vn;
     m0 = m0n;
     n0 = n0n;
+    rev = k_rev(n0);
     int ln = lane;
     asm volatile("" : "+v"(ln));
     set_tile(m0, n0, ln);

@@ -94,6 +94,95 @@ def test_summarize_scales_and_averages(tmp_path, capsys):
     assert "mfma_peak" not in json.dumps(res["stages"])
 
 
+def test_summarize_splits_forwards(tmp_path, capsys):
+    # a run of three forwards (the timed step and two telemetry steps): every
+    # forward's stages count, none of the later GEMMs is taken for the head
+    fetch, write = [], []
+    for fwd in range(3):
+        for n in _forward_names(L):
+            f = 1000.0 + fwd if n == G % 4 else (50.0 if "coherence" in n else 10.0)
+            fetch.append((n, f))
+            write.append((n, 20.0))
+    _write_counters(str(tmp_path / "tf"), "FETCH_SIZE", fetch)
+    _write_counters(str(tmp_path / "tw"), "WRITE_SIZE", write)
+    _write_counters(str(tmp_path / "cf"), "FETCH_SIZE", [("copy", 1024.0)])
+    _write_counters(str(tmp_path / "cw"), "WRITE_SIZE", [("copy", 1024.0)])
+    args = argparse.Namespace(summarize=[str(tmp_path / x) for x in ("tf", "tw", "cf", "cw")],
+                              copy_bytes=float(1 << 20))
+    bench.summarize(args)
+    import json
+    st = json.loads(capsys.readouterr().out)["stages"]
+    assert st["w13_gemm_silu"]["launches"] == 3 * L
+    assert st["w13_gemm_silu"]["fetch_bytes"] == 1001 * 1024
+    assert st["head_gemm"]["launches"] == 3 and st["embed"]["launches"] == 3
+    assert st["attention"]["launches"] == 3 * L
+    assert st["coherence"]["fetch_bytes"] == 50 * 1024
+
+
+_FAKE_ROCPROF = r"""#!%(py)s
+# stands in for rocprofv3 --pmc: writes a counter CSV for the command after --
+import csv, os, sys, time
+a = sys.argv[1:]
+counter, out = a[a.index("--pmc") + 1], a[a.index("-d") + 1]
+prog = a[a.index("--") + 1:]
+mode = os.environ.get("FAKE_ROCPROF_MODE", "ok")
+if mode == "hang":
+    time.sleep(60)
+if mode == "empty":
+    sys.exit(0)
+names = ["copy"] if "--copy-probe" in prog else %(names)r
+os.makedirs(os.path.join(out, "host"), exist_ok=True)
+with open(os.path.join(out, "host", "p_counter_collection.csv"), "w", newline="") as f:
+    w = csv.DictWriter(f, ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+    w.writeheader()
+    for i, n in enumerate(names):
+        v = 1024.0 if n == "copy" else (3000.0 if "4>" in n else 10.0)
+        if counter == "WRITE_SIZE":
+            v = 2048.0 if n == "copy" else v / 2
+        w.writerow({"Dispatch_Id": i + 1, "Kernel_Name": n, "Counter_Name": counter,
+                    "Counter_Value": v})
+# rocprofv3 may exit non-zero after writing whole results
+sys.exit(139 if mode == "segv" else 0)
+"""
+
+
+def _fake_rocprof(tmp_path, monkeypatch, mode):
+    import sys as _sys
+    d = tmp_path / "bin"
+    d.mkdir()
+    exe = d / "rocprofv3"
+    exe.write_text(_FAKE_ROCPROF % {"py": _sys.executable, "names": _forward_names(L) * 2})
+    exe.chmod(0o755)
+    monkeypatch.setenv("PATH", str(d) + os.pathsep + os.environ.get("PATH", ""))
+    monkeypatch.setenv("FAKE_ROCPROF_MODE", mode)
+    return argparse.Namespace(batch=16, seq=8192, window=512, threshold=1.335,
+                              copy_bytes=float(1 << 21))
+
+
+@pytest.mark.parametrize("mode", ["ok", "segv"])
+def test_live_traffic_runs_the_four_passes(tmp_path, monkeypatch, mode):
+    args = _fake_rocprof(tmp_path, monkeypatch, mode)
+    res, err = bench.live_traffic(args, timeout_s=60)
+    assert err is None
+    # copy: 2 MiB moved, FETCH_SIZE reads 1024 KiB (factor 2), WRITE_SIZE 2048 KiB (1)
+    assert res["fetch_scale"] == pytest.approx(2.0) and res["write_scale"] == pytest.approx(1.0)
+    w13 = res["stages"]["w13_gemm_silu"]
+    assert w13["launches"] == 2 * L
+    assert (w13["fetch_bytes"], w13["write_bytes"]) == (3000 * 1024 * 2, 1500 * 1024)
+
+
+def test_live_traffic_reports_failures(tmp_path, monkeypatch):
+    args = _fake_rocprof(tmp_path, monkeypatch, "empty")
+    res, err = bench.live_traffic(args, timeout_s=60)
+    assert res is None and "no usable counter output" in err
+    monkeypatch.setenv("FAKE_ROCPROF_MODE", "hang")
+    res, err = bench.live_traffic(args, timeout_s=2)
+    assert res is None and "timed out" in err
+    monkeypatch.setenv("PATH", str(tmp_path / "nowhere"))
+    res, err = bench.live_traffic(args)
+    assert res is None and "not on PATH" in err
+
+
 def test_summarize_trace_means_per_stage(tmp_path, capsys):
     # a probe before the first forward, then two forwards: W1|W3 launches take
     # 700 us in the first and 800 us in the second, every other kernel 10 us
