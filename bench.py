@@ -107,6 +107,7 @@ def summarize_dirs(dirs, copy_bytes, L=14):
     kf, kw = copy_bytes / (cf * 1024.0), copy_bytes / (cw * 1024.0)
     res = {"fetch_scale": kf, "write_scale": kw, "copy_bytes": copy_bytes,
            "copy_fetch_kib": cf, "copy_write_kib": cw, "stages": {}}
+    counts = {}
     for lst, key, k in ((fetch, "fetch_bytes", kf), (write, "write_bytes", kw)):
         ours = [(n, v) for n, v in lst if "blt::" in n]
         for st, (n, v) in zip(_forward_stages([n for n, _ in ours], L), ours):
@@ -114,11 +115,16 @@ def summarize_dirs(dirs, copy_bytes, L=14):
                 continue
             d = res["stages"].setdefault(st, {"launches": 0})
             d[key] = d.get(key, 0.0) + v * 1024.0 * k
-            if key == "fetch_bytes":
-                d["launches"] += 1
-    for d in res["stages"].values():
-        for key in ("fetch_bytes", "write_bytes"):
-            d[key] = round(d.get(key, 0.0) / max(d["launches"], 1))
+            counts[(st, key)] = counts.get((st, key), 0) + 1
+    # each counter's total over its own dispatches; a stage whose write pass
+    # saw a different number of launches than its fetch pass says so
+    for st, d in res["stages"].items():
+        nf, nw = counts.get((st, "fetch_bytes"), 0), counts.get((st, "write_bytes"), 0)
+        d["launches"] = nf
+        if nw != nf:
+            d["write_launches"] = nw
+        d["fetch_bytes"] = round(d.get("fetch_bytes", 0.0) / max(nf, 1))
+        d["write_bytes"] = round(d.get("write_bytes", 0.0) / max(nw, 1))
     return res
 
 
@@ -162,13 +168,17 @@ def live_traffic(args, timeout_s=180):
                     proc.wait()
                     return None, "rocprofv3 --pmc %s timed out after %d s" % (counter, timeout_s)
             # rocprofv3 can exit non-zero after the program ended with its
-            # results written; the summary below checks they are whole
+            # results written; the checks below take them only when whole
             if rc != 0:
                 print("bench: rocprofv3 --pmc %s exited %d" % (counter, rc), file=sys.stderr)
         try:
             res = summarize_dirs([os.path.join(tmp, d) for d, _, _ in runs], args.copy_bytes)
         except (IndexError, KeyError, ValueError, OSError) as e:
             return None, "no usable counter output (%s: %s)" % (type(e).__name__, e)
+        partial = sorted(st for st, d in res["stages"].items() if "write_launches" in d)
+        if partial:
+            return None, "FETCH_SIZE and WRITE_SIZE passes saw different launches of %s" % (
+                ", ".join(partial))
         return res, None
     finally:
         shutil.rmtree(tmp, ignore_errors=True)

@@ -131,6 +131,8 @@ if mode == "hang":
 if mode == "empty":
     sys.exit(0)
 names = ["copy"] if "--copy-probe" in prog else %(names)r
+if mode == "partial" and counter == "WRITE_SIZE" and "--copy-probe" not in prog:
+    names = names[:len(names) // 2]
 os.makedirs(os.path.join(out, "host"), exist_ok=True)
 with open(os.path.join(out, "host", "p_counter_collection.csv"), "w", newline="") as f:
     w = csv.DictWriter(f, ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
@@ -171,10 +173,30 @@ def test_live_traffic_runs_the_four_passes(tmp_path, monkeypatch, mode):
     assert (w13["fetch_bytes"], w13["write_bytes"]) == (3000 * 1024 * 2, 1500 * 1024)
 
 
+def test_summarize_averages_each_counter_over_its_own_launches(tmp_path, capsys):
+    # the write pass lost the second forward's dispatches: its bytes are still
+    # per launch, and the stage says how many launches each pass saw
+    names = _forward_names(L)
+    fetch = [(n, 1000.0 if n == G % 4 else 10.0) for n in names * 2]
+    write = [(n, 500.0 if n == G % 4 else 20.0) for n in names]
+    _write_counters(str(tmp_path / "tf"), "FETCH_SIZE", fetch)
+    _write_counters(str(tmp_path / "tw"), "WRITE_SIZE", write)
+    _write_counters(str(tmp_path / "cf"), "FETCH_SIZE", [("copy", 1024.0)])
+    _write_counters(str(tmp_path / "cw"), "WRITE_SIZE", [("copy", 1024.0)])
+    res = bench.summarize_dirs([str(tmp_path / x) for x in ("tf", "tw", "cf", "cw")],
+                               float(1 << 20))
+    w13 = res["stages"]["w13_gemm_silu"]
+    assert (w13["launches"], w13["write_launches"]) == (2 * L, L)
+    assert (w13["fetch_bytes"], w13["write_bytes"]) == (1000 * 1024, 500 * 1024)
+
+
 def test_live_traffic_reports_failures(tmp_path, monkeypatch):
     args = _fake_rocprof(tmp_path, monkeypatch, "empty")
     res, err = bench.live_traffic(args, timeout_s=60)
     assert res is None and "no usable counter output" in err
+    monkeypatch.setenv("FAKE_ROCPROF_MODE", "partial")
+    res, err = bench.live_traffic(args, timeout_s=60)
+    assert res is None and "different launches" in err
     monkeypatch.setenv("FAKE_ROCPROF_MODE", "hang")
     res, err = bench.live_traffic(args, timeout_s=2)
     assert res is None and "timed out" in err
