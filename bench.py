@@ -184,6 +184,58 @@ def live_traffic(args, timeout_s=180):
         shutil.rmtree(tmp, ignore_errors=True)
 
 
+def summarize_counters(dir1, dir2, layers=14):
+    """Per-stage SQ counter means of two rocprofv3 --pmc passes over the same
+    bench run (pass 1: SQ_WAVES, SQ_BUSY_CYCLES, SQ_ACTIVE_INST_VALU,
+    SQ_VALU_MFMA_BUSY_CYCLES, SQ_VALU_MFMA_COEXEC_CYCLES; pass 2: SQ_INSTS_VALU,
+    SQ_INSTS_MFMA, SQ_INSTS_SALU, SQ_INSTS_LDS, SQ_LDS_BANK_CONFLICT,
+    SQ_ACTIVE_INST_LDS), as a markdown table.  MI355X has 32 shader engines
+    and 1024 SIMDs: busy cycles per SE = SQ_BUSY_CYCLES / 32; MFMA busy =
+    SQ_VALU_MFMA_BUSY_CYCLES / (busy * 1024); VALU busy = 4 *
+    SQ_ACTIVE_INST_VALU (quad-cycles) / (busy * 1024); VALU beside MFMA =
+    SQ_VALU_MFMA_COEXEC_CYCLES / (busy * 1024); instructions per wave =
+    SQ_INSTS_* / SQ_WAVES."""
+    import csv
+    import glob
+
+    def load(d):
+        f = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)[0]
+        disp = {}
+        for r in csv.DictReader(open(f)):
+            e = disp.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"]})
+            e[r["Counter_Name"]] = float(r["Counter_Value"])
+        ours = [v for _, v in sorted(disp.items()) if "blt::" in v["name"]]
+        return list(zip(_forward_stages([v["name"] for v in ours], layers), ours))
+
+    p1, p2 = load(dir1), load(dir2)
+    if [st for st, _ in p1] != [st for st, _ in p2]:
+        raise ValueError("the two passes saw different dispatches")
+    tot, n = {}, {}
+    for (st, a), (_, b) in zip(p1, p2):
+        if st is None:
+            continue
+        t = tot.setdefault(st, {})
+        for k, v in list(a.items()) + list(b.items()):
+            if k != "name":
+                t[k] = t.get(k, 0.0) + v
+        n[st] = n.get(st, 0) + 1
+    lines = ["| stage | launches | busy cycles / SE | MFMA busy | VALU busy | VALU beside MFMA | "
+             "neither | VALU / wave | MFMA / wave | SALU / wave | LDS / wave | "
+             "LDS conflict / LDS active |", "|---" * 12 + "|"]
+    for st in sorted(tot, key=lambda k: -tot[k]["SQ_BUSY_CYCLES"]):
+        m = {k: v / n[st] for k, v in tot[st].items()}
+        busy = m["SQ_BUSY_CYCLES"] / 32.0
+        mf = m["SQ_VALU_MFMA_BUSY_CYCLES"] / (busy * 1024)
+        va = 4 * m["SQ_ACTIVE_INST_VALU"] / (busy * 1024)
+        co = m["SQ_VALU_MFMA_COEXEC_CYCLES"] / (busy * 1024)
+        w = m["SQ_WAVES"]
+        lines.append("| %s | %d | %d | %.1f%% | %.1f%% | %.1f%% | %.1f%% | %d | %d | %d | %d | %.2f |" % (
+            st, n[st], busy, 100 * mf, 100 * va, 100 * co, 100 * (1 - mf - va + co),
+            m["SQ_INSTS_VALU"] / w, m["SQ_INSTS_MFMA"] / w, m["SQ_INSTS_SALU"] / w,
+            m["SQ_INSTS_LDS"] / w, m["SQ_LDS_BANK_CONFLICT"] / max(m["SQ_ACTIVE_INST_LDS"], 1.0)))
+    return "\n".join(lines)
+
+
 def summarize_trace(path):
     """Per-stage mean kernel duration from a rocprofv3 --kernel-trace CSV of
     bench.py (stages recovered from the dispatch order of each forward)."""
@@ -257,6 +309,8 @@ def main():
                                                      "COPY_WRITE_DIR"),
                     help="print per-stage traffic from rocprofv3 --pmc output and exit")
     ap.add_argument("--copy-bytes", type=float, default=float(2 ** 30))
+    ap.add_argument("--summarize-counters", nargs=2, metavar=("PASS1_DIR", "PASS2_DIR"),
+                    help="print per-stage SQ counter means of two rocprofv3 --pmc passes")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                     help="print per-stage kernel durations from rocprofv3 --kernel-trace output")
     ap.add_argument("--copy-probe", action="store_true",
@@ -274,6 +328,9 @@ def main():
         return
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
+        return
+    if args.summarize_counters:
+        print(summarize_counters(*args.summarize_counters))
         return
     if args.summarize:
         summarize(args)

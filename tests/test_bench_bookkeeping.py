@@ -205,6 +205,51 @@ def test_live_traffic_reports_failures(tmp_path, monkeypatch):
     assert res is None and "not on PATH" in err
 
 
+def _write_multi(d, rows):
+    os.makedirs(os.path.join(d, "host"), exist_ok=True)
+    with open(os.path.join(d, "host", "p_counter_collection.csv"), "w", newline="") as f:
+        w = csv.DictWriter(f, ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+        w.writeheader()
+        for i, (name, counters) in enumerate(rows):
+            for c, v in counters.items():
+                w.writerow({"Dispatch_Id": i + 1, "Kernel_Name": name, "Counter_Name": c,
+                            "Counter_Value": v})
+
+
+def test_summarize_counters_normalises_per_stage(tmp_path):
+    # W1|W3 launches: 32,000 busy cycles summed over 32 SEs (1,000 per SE); the
+    # matrix core busy 512,000 SIMD cycles of 1,024,000 (50 %), VALU 64,000
+    # quad-cycles (25 %), 102,400 cycles of both (10 %); 100 waves issuing 500
+    # VALU, 120 MFMA, 300 SALU, 80 LDS instructions each
+    names = _forward_names(L)
+    p1, p2 = [], []
+    for n in names:
+        if n == G % 4:
+            p1.append((n, {"SQ_WAVES": 100, "SQ_BUSY_CYCLES": 32000, "SQ_ACTIVE_INST_VALU": 64000,
+                           "SQ_VALU_MFMA_BUSY_CYCLES": 512000,
+                           "SQ_VALU_MFMA_COEXEC_CYCLES": 102400}))
+            p2.append((n, {"SQ_INSTS_VALU": 50000, "SQ_INSTS_MFMA": 12000, "SQ_INSTS_SALU": 30000,
+                           "SQ_INSTS_LDS": 8000, "SQ_LDS_BANK_CONFLICT": 5,
+                           "SQ_ACTIVE_INST_LDS": 20}))
+        else:
+            p1.append((n, {"SQ_WAVES": 1, "SQ_BUSY_CYCLES": 32, "SQ_ACTIVE_INST_VALU": 0,
+                           "SQ_VALU_MFMA_BUSY_CYCLES": 0, "SQ_VALU_MFMA_COEXEC_CYCLES": 0}))
+            p2.append((n, {"SQ_INSTS_VALU": 1, "SQ_INSTS_MFMA": 0, "SQ_INSTS_SALU": 1,
+                           "SQ_INSTS_LDS": 0, "SQ_LDS_BANK_CONFLICT": 0, "SQ_ACTIVE_INST_LDS": 0}))
+    _write_multi(str(tmp_path / "a"), p1)
+    _write_multi(str(tmp_path / "b"), p2)
+    table = bench.summarize_counters(str(tmp_path / "a"), str(tmp_path / "b"), L)
+    rows = {r.split("|")[1].strip(): [c.strip() for c in r.split("|")[2:-1]]
+            for r in table.splitlines()[2:]}
+    assert rows["w13_gemm_silu"] == ["%d" % L, "1000", "50.0%", "25.0%", "10.0%", "35.0%", "500",
+                                     "120", "300", "80", "0.25"]
+    assert list(rows)[0] == "w13_gemm_silu"  # most busy cycles first
+    # passes over different dispatches are refused
+    _write_multi(str(tmp_path / "c"), p2[:-1])
+    with pytest.raises(ValueError):
+        bench.summarize_counters(str(tmp_path / "a"), str(tmp_path / "c"), L)
+
+
 def test_summarize_trace_means_per_stage(tmp_path, capsys):
     # a probe before the first forward, then two forwards: W1|W3 launches take
     # 700 us in the first and 800 us in the second, every other kernel 10 us
