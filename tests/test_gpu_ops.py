@@ -574,12 +574,14 @@ def test_gemm_f32_epilogue_partial_columns(M, N):
     assert (c - ref).abs().max().item() <= 2e-3 * ref.abs().max().item()
 
 
+@pytest.mark.parametrize("K", [192, 768])
 @pytest.mark.parametrize("epi", ["bf16", "resid", "f32", "silu", "qkv"])
-def test_gemm_small_launch_tiles_bit_identical(epi):
+def test_gemm_small_launch_tiles_bit_identical(epi, K):
     # A launch with fewer 256 x 256 tiles than CUs runs on 128 x 128 tiles; its
     # rows must equal the same rows of a launch that stays on 256 x 256 tiles,
-    # bit for bit (the model's row-independence rests on it).
-    K, Mb, Ms = 768, 256 * 256 + 64, 1000
+    # bit for bit (the model's row-independence rests on it), also on the
+    # column blocks whose K tiles run from the last one down (N > 1024).
+    Mb, Ms = 256 * 256 + 64, 1000
     N = {"silu": 4096, "qkv": 2304}.get(epi, 768)
     torch.manual_seed(5)
     a = torch.randn(Mb, K, device=DEV).to(torch.bfloat16)
@@ -620,13 +622,18 @@ def test_probe_copy_and_mfma():
 
 
 # ---------------------------------------------------------------- persistent GEMM tile walks
+@pytest.mark.parametrize("N", [512, 2304])
 @pytest.mark.parametrize("K", [64, 192, 320, 768])
-def test_gemm_persistent_many_tiles_odd_k_tiles(K):
+def test_gemm_persistent_many_tiles_odd_k_tiles(K, N):
     # More tiles than CUs (each block walks several tiles) with odd and even
     # numbers of 64-deep K tiles, so the LDS stage holding a tile's last K
     # tile alternates between tiles; a ragged last row tile.  Every epilogue
-    # kind on the same operands.
-    M, N = 256 * 133 + 17, 512
+    # kind on the same operands.  N = 2304: column tiles 4-7 (first column
+    # with bit 10 set) take their K tiles from the last one down, and the row
+    # tiles go in groups of 8 whose odd members walk the columns in reverse
+    # (134 row tiles: a partial last group), so a block's next tile can run
+    # the other K direction, including with a single K tile.
+    M = 256 * 133 + 17
     torch.manual_seed(K)
     a = torch.randn(M, K, device=DEV).to(torch.bfloat16)
     bt = (0.1 * torch.randn(N, K, device=DEV)).to(torch.bfloat16)
