@@ -137,9 +137,9 @@ def live_traffic(args, timeout_s=180):
     """Config 4's per-stage traffic measured in this run: the four rocprofv3
     --pmc passes that --summarize reads (one counter each: FETCH_SIZE, then
     WRITE_SIZE, over a one-step bench of the same shape, then both over the
-    copy probe), each a child process under its own time limit.  Called
-    before this process touches the GPU.  Returns (summary, None) or
-    (None, reason)."""
+    copy probe), each a child process; all four share one time limit of
+    timeout_s seconds.  Called before this process touches the GPU.  Returns
+    (summary, None) or (None, reason)."""
     import shutil
     import signal
     import subprocess
@@ -154,6 +154,7 @@ def live_traffic(args, timeout_s=180):
     probe = ["--copy-probe", "--copy-bytes", repr(args.copy_bytes)]
     runs = (("tf", "FETCH_SIZE", step), ("tw", "WRITE_SIZE", step),
             ("cf", "FETCH_SIZE", probe), ("cw", "WRITE_SIZE", probe))
+    deadline = time.monotonic() + timeout_s
     try:
         for d, counter, extra in runs:
             cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", os.path.join(tmp, d),
@@ -162,11 +163,12 @@ def live_traffic(args, timeout_s=180):
                 proc = subprocess.Popen(cmd, stdout=log, stderr=subprocess.STDOUT,
                                         start_new_session=True, cwd=tmp)
                 try:
-                    rc = proc.wait(timeout=timeout_s)
+                    rc = proc.wait(timeout=max(deadline - time.monotonic(), 0.1))
                 except subprocess.TimeoutExpired:
                     os.killpg(proc.pid, signal.SIGKILL)
                     proc.wait()
-                    return None, "rocprofv3 --pmc %s timed out after %d s" % (counter, timeout_s)
+                    return None, "rocprofv3 --pmc passes over their %d s limit (at %s)" % (
+                        timeout_s, counter)
             # rocprofv3 can exit non-zero after the program ended with its
             # results written; the checks below take them only when whole
             if rc != 0:
