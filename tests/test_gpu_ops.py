@@ -380,25 +380,31 @@ def _assert_rows_close(o, ref, rel=2e-2, label=""):
     (1, 1, 130, False, 0, 0.0), (1, 2, 300, True, 0, 10000.0), (2, 2, 700, True, 512, 10000.0),
     (1, 1, 1, True, 0, 10000.0), (1, 1, 97, True, 1, 0.0),
     # RoPE slices of uneven size: 3 batch slices; 4 head slices of 5 heads
-    (3, 2, 300, True, 64, 10000.0), (1, 5, 200, True, 0, 10000.0)])
+    (3, 2, 300, True, 64, 10000.0), (1, 5, 200, True, 0, 10000.0),
+    # window edges at any offset inside a 64-key tile
+    (1, 2, 500, True, 100, 10000.0), (2, 1, 777, True, 333, 0.0)])
 def test_attention_vs_oracle(B, H, T, causal, window, theta):
     o, ref = _attn_case(B, H, T, causal, window, theta)
     _assert_rows_close(o, ref, label="B%d H%d T%d w%d" % (B, H, T, window))
 
 
+@pytest.mark.parametrize("W,val,periods", [(512, 512.0, (61, 63, 50)),
+                                           (300, 256.0, (61, 63, 47))])
 @pytest.mark.parametrize("theta", [0.0, 10000.0])
-def test_attention_window_edge(theta):
+def test_attention_window_edge(theta, W, val, periods):
     # q = k = 0: every visible key gets the same weight, so row i of the output
     # is the mean of v over keys j in (i - W, i].  v[j] is one-hot in column
-    # j % P (value W, exact in bf16) with a period P per head that does not
+    # j % P (value val, exact in bf16) with a period P per head that does not
     # divide W, so including key i - W or dropping key i - W + 1 (or i) moves
-    # some column of every row with i >= W by about 1 against outputs of ~8.
-    # Expected values in closed form, independent of the oracle.
-    W, T, H = 512, 1600, 3
-    periods = (61, 63, 50)
+    # some column of every row with i >= W by about val / W against outputs
+    # of about val / P.  W = 300 puts the window edge at varying offsets inside
+    # the 64-key tiles.  Expected values in closed form, independent of the
+    # oracle.
+    T, H = 1600, 3
+    assert all(W % P for P in periods)
     v = np.zeros((1, H, T, 64), np.float32)
     for h, P in enumerate(periods):
-        v[0, h, np.arange(T), np.arange(T) % P] = W
+        v[0, h, np.arange(T), np.arange(T) % P] = val
     z = torch.zeros((1, H, T, 64), dtype=torch.bfloat16, device=DEV)
     o = F.fused_attention(z, z, torch.from_numpy(v).to(DEV).to(torch.bfloat16), True,
                           window=W, rope_theta=theta).float().cpu().numpy()
@@ -406,7 +412,7 @@ def test_attention_window_edge(theta):
     for h, P in enumerate(periods):
         for i in range(T):
             j = np.arange(max(0, i - W + 1), i + 1)
-            want[0, h, i] = np.bincount(j % P, minlength=64)[:64] * W / len(j)
+            want[0, h, i] = np.bincount(j % P, minlength=64)[:64] * val / len(j)
     np.testing.assert_allclose(o, want, rtol=2 ** -8, atol=1e-3)
     # the oracle agrees with the closed form (no rounding anywhere on its side)
     ref = oracle.attention(np.zeros_like(v), np.zeros_like(v), v, True, W, theta)
