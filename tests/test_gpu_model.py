@@ -64,7 +64,7 @@ def _compare(out, ref, label):
         np.testing.assert_array_equal(mask, oracle.patch_mask(H, thr, mode))
 
 
-@pytest.mark.parametrize("window", [0, 32])
+@pytest.mark.parametrize("window", [0, 32, 100])
 def test_tiny_model(window):
     cfg = M.LMTransformerConfig(dim=128, n_layers=2, n_heads=2, ffn_dim_multiplier=2.0,
                                 multiple_of=64, max_seqlen=512, vocab_size=260)
@@ -72,7 +72,7 @@ def test_tiny_model(window):
     _compare(out, ref, "tiny w=%d" % window)
 
 
-@pytest.mark.parametrize("window,T", [(0, 256), (512, 700)])
+@pytest.mark.parametrize("window,T", [(0, 256), (512, 700), (300, 700)])
 def test_entropy_model_dims(window, T):
     # the BLT entropy model at real size (14 x 768, 12 heads, FFN 2048, V 260), short T
     cfg = M.entropy_model_config()
